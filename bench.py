@@ -1,0 +1,351 @@
+"""W4A16 benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]        # the contract line
+    python bench.py --sweep skinny [--out FILE]                # M = 1..64, three ways
+    python bench.py --no-cpu --steps 50                        # shorter run (profiling)
+
+Workload (the M=1 GEMV sweep over the Qwen2.5-1.5B and 3B decoder projections): one step is an
+M=1 ops.linear (the deployed path: the v6 GEMV on the device layout) over every projection of one 1.5B decoder layer
+and one 3B decoder layer -- q, k, v, o, gate, up, down at (K, N) = (1536|2048, ...) -- i.e. 14 launches. Weights are
+random N(0, 0.02), int4 g128 with the per-group clip search (GPU quantizer), x ~ N(0, 1) fp16. Step i reads layer copy
+i mod C, with C distinct copies sized so the rotation covers >= 1 GiB, so no weight is served from the 256 MB
+Infinity Cache. The K timed steps run as one hipGraph replay (torch.cuda.CUDAGraph) between two synchronizations.
+
+value = algorithmic bytes moved per step (int4 weights + fp16 scales + x + y, reference bench/gpu_run.py:255,267)
+x K / elapsed, in GB/s: whole-job throughput including the per-kernel launch gap of the graph.
+roofline = the GEMV kernel alone: the same bytes / its own duration, timed by HIP events bound to each dispatch
+(lowbit_w4_gemv_timed), over K further eager steps on the launch stream; peak = 8 TB/s (MI355X HBM3E).
+cpu_baseline = the reference's CPU path (oracle: dequantize to fp16, then torch.nn.functional.linear on the host) on a
+bounded sample of the same steps.
+"""
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT / "lowbit-kernels_amd", ROOT):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+GROUP = 128
+CLIP_GRID = tuple(round(1.0 - 0.025 * i, 3) for i in range(11))       # reference bench/e2e.py:30
+HBM_PEAK_GBPS = 8000.0
+MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
+
+
+def step_projections():
+    out = []
+    for name, (h, inter) in MODELS.items():
+        kv = 2 * 128
+        out += [(f"{name}.q", h, h), (f"{name}.k", h, kv), (f"{name}.v", h, kv), (f"{name}.o", h, h),
+                (f"{name}.gate", h, inter), (f"{name}.up", h, inter), (f"{name}.down", inter, h)]
+    return out
+
+
+def w4_bytes(k, n):
+    return n * k // 2 + n * (k // GROUP) * 2
+
+
+def alg_bytes(k, n, m=1):
+    return w4_bytes(k, n) + 2 * (m * k + m * n)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 BLAS step")
+    ap.add_argument("--sweep", choices=["skinny"], default=None)
+    ap.add_argument("--out", default=None)
+    return ap.parse_args()
+
+
+class HipEvents:
+    """hipEvent_t pairs through libamdhip64 (the events lowbit_w4_gemv_timed binds to a dispatch)."""
+
+    def __init__(self, n):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.ev = []
+        for _ in range(2 * n):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            self.ev.append(e)
+
+    def pair(self, i):
+        return self.ev[2 * i], self.ev[2 * i + 1]
+
+    def elapsed_ms(self, i):
+        a, b = self.pair(i)
+        if self.hip.hipEventSynchronize(b) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def close(self):
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+
+
+def build_pool(torch, ops, projs, gib=1.0, fp16=False, seed=0):
+    """C layer copies (list of dicts name -> W4Weight, and optionally name -> fp16 weight), C covering >= gib GiB."""
+    per_copy = sum(w4_bytes(k, n) for _, k, n in projs)
+    copies = int(-(-gib * 2 ** 30 // per_copy)) + 1
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    pool, pool16, host = [], [], []
+    for c in range(copies):
+        layer, layer16, layer_host = {}, {}, {}
+        for name, k, n in projs:
+            w = torch.randn(n, k, generator=gen, device="cuda") * 0.02
+            packed, scales = ops.quantize_w4_gpu(w, GROUP, CLIP_GRID)
+            layer[name] = ops.W4Weight(packed, scales, GROUP, ("mma",), device=packed.device)
+            if fp16:
+                layer16[name] = ops.dequantize_w4_gpu(packed, scales, GROUP)
+            if c < 2:                       # canonical host copies for the CPU baseline
+                layer_host[name] = (packed.cpu().numpy(), scales.cpu().numpy())
+            del w, packed
+        pool.append(layer)
+        pool16.append(layer16)
+        if layer_host:
+            host.append(layer_host)
+    torch.cuda.synchronize()
+    return pool, pool16, host, copies
+
+
+def cpu_baseline(projs, host, xs, budget_s=15.0):
+    """The reference's CPU torch path on the host: dequantize (u - 8) * scale to fp16 (oracle,
+    reference lowbit/ops.py:119-123), then torch.nn.functional.linear -- timed over whole steps until budget_s."""
+    import torch
+    from oracle import quant_ref as R
+    xh = {name: x.cpu() for name, x in xs.items()}
+    threads = torch.get_num_threads()
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        layer = host[steps % len(host)]
+        for name, k, n in projs:
+            packed, scales = layer[name]
+            w16 = torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP))
+            torch.nn.functional.linear(xh[name], w16)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    step_bytes = sum(alg_bytes(k, n) for _, k, n in projs)
+    return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} steps of the same 14-projection M=1 sweep ({step_bytes / 1e6:.1f} MB each): oracle "
+                      f"dequant to fp16 + torch.nn.functional.linear on {threads} host threads, {el:.1f} s",
+            "ms_per_step": round(1000 * el / steps, 3)}
+
+
+def contract(a):
+    import torch
+    from lowbit import _native, ops
+    from oracle import quant_ref as R
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    projs = step_projections()
+    step_bytes = sum(alg_bytes(k, n) for _, k, n in projs)
+    pool, pool16, host, copies = build_pool(torch, ops, projs, fp16=not a.no_fp16)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    xs = {name: torch.randn(1, k, generator=gen, device="cuda").half() for name, k, n in projs}
+
+    # parity spot check before timing: every projection of copy 0 against the oracle's fp64 GEMV
+    for name, k, n in projs:
+        packed, scales = host[0][name]
+        ref = R.gemv_reference(xs[name].double().cpu().numpy(), packed, scales, GROUP)
+        err = R.rel_err(ops.linear(xs[name], pool[0][name]).cpu().numpy(), ref)
+        if err > R.REL_BOUND:
+            raise SystemExit(f"parity check failed on {name}: {err:.2e}")
+
+    def step(i):
+        layer = pool[i % copies]
+        for name, k, n in projs:
+            ops.linear(xs[name], layer[name])
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # the K timed steps as one graph replay
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step(0)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(a.steps):
+            step(i)
+    graph.replay()                                   # one untimed replay: instantiation and first-touch costs
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    elapsed_ms = e0.elapsed_time(e1)
+    del graph
+
+    # kernel-only durations: events bound to each GEMV dispatch, on the launch stream
+    lib = _native.lib()
+    ev = HipEvents(len(projs))
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    ys = {name: torch.empty(1, n, dtype=torch.float16, device=dev) for name, k, n in projs}
+    per = {name: [] for name, _, _ in projs}
+    for i in range(a.steps):
+        layer = pool[i % copies]
+        for j, (name, k, n) in enumerate(projs):
+            wq = layer[name]
+            e_start, e_stop = ev.pair(j)
+            _native.check(lib.lowbit_w4_gemv_timed(_native.ptr(xs[name]), _native.ptr(wq.packed_mma),
+                                                   _native.ptr(wq.scales), _native.ptr(ys[name]), 1, n, k, GROUP, 6, 0,
+                                                   sp, e_start, e_stop))
+        for j, (name, k, n) in enumerate(projs):
+            per[name].append(ev.elapsed_ms(j))
+    ev.close()
+    kernel_ms = sum(sum(v) for v in per.values())
+    launches = sum(len(v) for v in per.values())
+    achieved = step_bytes * a.steps / (kernel_ms / 1e3) / 1e9
+
+    # fp16 BLAS on the same cold rotation (dequantized weights), one graph of K steps
+    fp16 = None
+    if pool16 and pool16[0]:
+        def step16(i):
+            layer = pool16[i % copies]
+            for name, k, n in projs:
+                torch.nn.functional.linear(xs[name], layer[name])
+        step16(0)
+        torch.cuda.synchronize()
+        g16 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g16):
+            for i in range(a.steps):
+                step16(i)
+        g16.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        g16.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        fp16 = e0.elapsed_time(e1) / a.steps
+        del g16
+
+    detail = {}
+    for name, k, n in projs:
+        shape = name.split(".", 1)[1]
+        if shape in ("v", "up"):
+            continue                                       # same shapes as k and gate
+        us = 1000 * sum(per[name]) / len(per[name])
+        detail[f"{name}({k}x{n})"] = {"kernel_us": round(us, 2), "GBps": round(alg_bytes(k, n) / (us * 1e-6) / 1e9, 1)}
+
+    line = {
+        "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1; us/call M=1..64 vs hipBLASLt fp16",
+        "value": round(step_bytes * a.steps / (elapsed_ms / 1e3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(elapsed_ms / a.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic: random N(0,0.02) weights (int4 g128, clip search), N(0,1) fp16 x, "
+                f"{copies} distinct layer copies ({copies * sum(w4_bytes(k, n) for _, k, n in projs) / 2**30:.2f} GiB) cycled",
+        "config": {"workload": "BASELINE configs[1]: M=1 GEMV over the 7 projections of one Qwen2.5-1.5B and one "
+                               "Qwen2.5-3B decoder layer per step (14 launches), hipGraph replay",
+                   "step_bytes": step_bytes, "M": 1, "group": GROUP, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "lowbit::gemv_mfma_layout<1,1,true>", "kernel_avg_us": round(1000 * kernel_ms / launches, 3),
+                     "launches": launches},
+        "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,
+        "speedup_vs_fp16_blas": round(fp16 / (elapsed_ms / a.steps), 3) if fp16 else None,
+        "blas_backend": str(torch.backends.cuda.preferred_blas_library()),
+        "detail": detail,
+    }
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(projs, host, xs)
+    print(json.dumps(line), flush=True)
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(line, indent=1))
+
+
+def sweep_skinny(a):
+    """M in {1,2,4,8,16,24,32,48,64} on 3B and 7B-shaped MLP layers; us/call for the v6 GEMV
+    (M <= 8), the MFMA kernel (v5), dequant + BLAS, and fp16 BLAS, each a graph cycling >= 1 GiB of copies."""
+    import torch
+    from lowbit import ops
+    torch.cuda.set_device(0)
+    shapes = [("3b.gate_up", 2048, 11008), ("3b.down", 11008, 2048), ("7b.gate_up", 3584, 18944), ("7b.down", 18944, 3584)]
+    ms = [1, 2, 4, 8, 16, 24, 32, 48, 64]
+    rows = []
+    for name, k, n in shapes:
+        projs = [(name, k, n)]
+        pool, pool16, _, copies = build_pool(torch, ops, projs, fp16=True, seed=k + n)
+        for m in ms:
+            x = torch.randn(m, k, device="cuda").half()
+            r = {"shape": name, "K": k, "N": n, "M": m, "copies": copies}
+
+            def timed(fn, iters=max(200, copies)):
+                fn(0)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for i in range(iters):
+                        fn(i)
+                g.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                best = 1e30
+                for _ in range(3):
+                    e0.record()
+                    g.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    best = min(best, e0.elapsed_time(e1) * 1000 / iters)
+                return round(best, 2)
+
+            if m <= 8:
+                r["gemv_v6_us"] = timed(lambda i: ops.gemv(x, pool[i % copies][name], 6))
+            r["mfma_v5_us"] = timed(lambda i: ops.gemv(x, pool[i % copies][name], 5))
+            r["dequant_blas_us"] = timed(lambda i: torch.nn.functional.linear(x, ops.dequant(pool[i % copies][name], "mma")))
+            r["fp16_blas_us"] = timed(lambda i: torch.nn.functional.linear(x, pool16[i % copies][name]))
+            r["linear_us"] = timed(lambda i: ops.linear(x, pool[i % copies][name]))
+            r["linear_path"] = ops.auto_version(m, pool[0][name]) or "dequant+blas"
+            r["int4_roofline_us"] = round(alg_bytes(k, n, m) / (HBM_PEAK_GBPS * 1e9) * 1e6, 2)
+            rows.append(r)
+            print(json.dumps(r), flush=True)
+        del pool, pool16
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {a.gpus}); the W4A16 path is not sharded in this build",
+              file=sys.stderr)
+        sys.exit(2)
+    if int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU only; launch it without torch.distributed.run", file=sys.stderr)
+        sys.exit(2)
+    if a.sweep == "skinny":
+        sweep_skinny(a)
+    else:
+        contract(a)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,118 @@
+/* lowbit_w4.h -- C ABI of liblowbit_w4.so, the gfx950 W4A16 kernel library.
+ *
+ * Format (reference lowbit/quant.py:1-35): a weight W [N, K] is stored as symmetric int4, one fp16 scale per group of
+ * G consecutive values along K (G % 32 == 0, K % G == 0), the nibble u = q + 8 two per byte, low nibble = even k.
+ * Three byte layouts of the packed tensor [N, K/2] exist:
+ *   LOWBIT_LAYOUT_CANONICAL  row-major bytes as quantized (reference "canonical", lowbit/quant.py:7-8);
+ *   LOWBIT_LAYOUT_V3         canonical with each 32-bit word in the nibble order [k0,k2,k4,k6,k1,k3,k5,k7]
+ *                            (reference interleave_for_gpu, lowbit/quant.py:55-64);
+ *   LOWBIT_LAYOUT_MFMA       this library's gfx950 device layout, the one copy a model keeps and the counterpart of
+ *                            the reference's "mma" layout (lowbit/quant.py:67-78): 16-row tiles; inside tile t, the
+ *                            128-k chunk c holds rows_t x 64 bytes (row r at offset 64 r), words in v3 order.
+ *                            Needs K % 128 == 0 and G % 128 == 0.
+ * Scales are always float16 [N, K/G], row-major.
+ *
+ * Conventions. Pointers are device pointers unless the function name says host. x, y and scales are IEEE binary16
+ * (passed as void*). `stream` is a hipStream_t (NULL = the default stream). Every entry point validates its
+ * arguments first and returns LOWBIT_OK (0) or a status code; lowbit_last_error() returns the message of the last
+ * failure on the calling thread (the same wording as the reference's TORCH_CHECK messages). No entry point
+ * allocates device memory: outputs are owned by the caller, so every launch can be captured into a hipGraph.
+ * Launches are asynchronous on `stream`.
+ */
+#ifndef LOWBIT_W4_H
+#define LOWBIT_W4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LOWBIT_OK = 0,
+  LOWBIT_ERR_ARG = 1,      /* a NULL pointer, a bad enum value, a non-positive size */
+  LOWBIT_ERR_GROUP = 2,    /* group size not positive / not a multiple of 32, or K not a multiple of it */
+  LOWBIT_ERR_SHAPE = 3,    /* inconsistent sizes */
+  LOWBIT_ERR_ALIGN = 4,    /* x / w not 16-byte aligned */
+  LOWBIT_ERR_ROWS = 5,     /* M outside the kernel's range */
+  LOWBIT_ERR_VERSION = 6,  /* unknown kernel version */
+  LOWBIT_ERR_LAYOUT = 7,   /* the MFMA layout needs K % 128 == 0 and G % 128 == 0 */
+  LOWBIT_ERR_TUNING = 8,   /* rows_per_wave / row_tiles not in the allowed set */
+  LOWBIT_ERR_HIP = 9,      /* a HIP runtime call or launch failed */
+  LOWBIT_ERR_DEVICE = 10   /* the current device is not gfx950 */
+};
+
+enum { LOWBIT_LAYOUT_CANONICAL = 0, LOWBIT_LAYOUT_V3 = 1, LOWBIT_LAYOUT_MFMA = 2, LOWBIT_LAYOUT_NV_MMA = 3 };
+enum { LOWBIT_DTYPE_F32 = 0, LOWBIT_DTYPE_F16 = 1, LOWBIT_DTYPE_BF16 = 2 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lowbit_last_error(void);
+/* Short name of a status code. */
+const char* lowbit_strerror(int status);
+/* Library version string. */
+const char* lowbit_version(void);
+
+/* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
+ * Replaces the reference's w4_gemv (csrc/w4_gemv.cu:454-484) and, through it, ops.gemv(version in 1..4, 6)
+ * (lowbit/ops.py:67-78). version 1 or 2: w in the canonical layout; 3 or 4: v3 layout; 6: the MFMA layout (needs
+ * K % 128 == 0 and G % 128 == 0). rows_per_wave: 0 = chosen from N and M, else 1, 2 or 4 (versions 1-4: output
+ * rows per wave; version 6: 16-row tiles per wave). fp32 accumulation. */
+int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+                   int version, int rows_per_wave, void* stream);
+
+/* y[M, N] (fp16) = x[M, K] . dequant(W)^T on the MFMA layout with fp16 MFMA (fp32 accumulate), 1 <= M <= 64.
+ * Replaces the reference's w4_gemm_tc (csrc/w4_gemv.cu:486-515), i.e. ops.gemv(version 5) (lowbit/ops.py:75-76).
+ * row_tiles: 0 = chosen from N and M, else 1, 2 or 4 sixteen-row tiles per wave. */
+int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                        int64_t group, int row_tiles, void* stream);
+
+/* out[N, K] (fp16) = (u - 8) * scale rounded once to fp16, from the canonical (mfma_layout = 0) or the MFMA layout
+ * (mfma_layout = 1). Both give the same bits. Replaces the reference's w4_dequant (csrc/w4_gemv.cu:517-540), i.e.
+ * ops.dequant (lowbit/ops.py:126-135). */
+int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_t K, int64_t group, int mfma_layout,
+                      void* stream);
+
+/* GPU quantizer: W [N, K] (float32, float16 or bfloat16 by w_dtype) -> packed canonical u8 [N, K/2] + fp16 scales
+ * [N, K/G]. clip_grid (HOST array of n_clip floats, may be NULL with n_clip = 0): per group, try
+ * scale = f16(f32(amax * a) / 7) for each a and keep the strictly smallest squared error (first wins ties); with
+ * no grid the result is bit-identical to the canonical absmax quantizer. Replaces the reference's
+ * ops.quantize_w4_gpu (lowbit/ops.py:81-116), which is torch code there. n_clip <= 64. */
+int lowbit_w4_quantize(const void* w, int w_dtype, void* packed, void* scales, int64_t N, int64_t K, int64_t group,
+                       const float* clip_grid, int n_clip, void* stream);
+
+/* Device relayout of packed weights: src canonical [N, K/2] -> dst in `layout` (LOWBIT_LAYOUT_V3 or
+ * LOWBIT_LAYOUT_MFMA; dst must not alias src). Replaces the host-side numpy interleave + copy the reference does in
+ * W4Weight (lowbit/ops.py:42-44, quant.interleave_for_gpu / interleave_for_mma). */
+int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int layout, void* stream);
+
+/* ---- host-side format functions (CPU memory, no GPU needed); counterparts of lowbit/quant.py ---- */
+
+/* quant.quantize_w4 (lowbit/quant.py:23-35): w float32 [N, K] -> packed [N, K/2], scales fp16 bits [N, K/G]. */
+int lowbit_host_quantize(const float* w, uint8_t* packed, uint16_t* scales, int64_t N, int64_t K, int64_t group);
+/* quant.unpack_w4 (lowbit/quant.py:38-44): packed [N, K/2] (canonical) -> int8 [N, K] in -8..7. */
+int lowbit_host_unpack(const uint8_t* packed, int8_t* out, int64_t N, int64_t K);
+/* quant.dequantize_w4 (lowbit/quant.py:47-51): float32 [N, K] = (u - 8) * scale. */
+int lowbit_host_dequantize(const uint8_t* packed, const uint16_t* scales, float* out, int64_t N, int64_t K,
+                           int64_t group);
+/* quant.interleave_for_gpu / interleave_for_mma (lowbit/quant.py:55-78) and this library's MFMA layout:
+ * canonical src [N, K/2] -> dst in layout (V3, NV_MMA = the reference's m16n8k8 fragment order, or MFMA). */
+int lowbit_host_relayout(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int layout);
+/* quant.gemv_reference (lowbit/quant.py:81-84): y float64 [M, N] = x float64 [M, K] . dequant(W)^T. */
+int lowbit_host_gemv_reference(const double* x, const uint8_t* packed, const uint16_t* scales, double* y, int64_t M,
+                               int64_t N, int64_t K, int64_t group);
+
+/* ---- timing support for the benchmark ----
+ * Same as lowbit_w4_gemv / lowbit_w4_gemm_mfma, but the launch carries start/stop hipEvent_t handles bound to the
+ * kernel dispatch itself (hipExtLaunchKernel), so their elapsed time is the kernel's own duration, without the
+ * queue gap in front of it. No counterpart in the reference (its harness timed CUDA-graph replays). */
+int lowbit_w4_gemv_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group, int version, int rows_per_wave, void* stream, void* start_event,
+                         void* stop_event);
+int lowbit_w4_gemm_mfma_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                              int64_t group, int row_tiles, void* stream, void* start_event, void* stop_event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOWBIT_W4_H */

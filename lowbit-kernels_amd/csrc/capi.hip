@@ -1,0 +1,197 @@
+// The C ABI (include/lowbit_w4.h): argument validation with the reference's messages, then dispatch to the kernels.
+// The validation mirrors the reference's check() / TORCH_CHECKs (csrc/w4_gemv.cu:312-325,454-540); checks that need
+// tensor metadata (device, dtype, contiguity, dims) are done by the Python layer, which owns the tensors.
+#include <climits>
+#include <cstring>
+
+#include "kernels.hpp"
+#include "lowbit_w4.h"
+#include "status.hpp"
+
+namespace lowbit {
+
+char* error_buffer() {
+  static thread_local char buf[512];
+  return buf;
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+int g_arch_ok[kMaxDevices];     // 0 unknown, 1 gfx950, -1 other (benign race: every writer stores the same value)
+
+int check_device() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return LOWBIT_OK;
+  if (g_arch_ok[dev] == 0) {
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "hipGetDeviceProperties failed: %s", hipGetErrorString(e));
+    g_arch_ok[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    if (g_arch_ok[dev] < 0)
+      return fail(LOWBIT_ERR_DEVICE, "liblowbit_w4 is built for gfx950 only; device %d is %s", dev, prop.gcnArchName);
+  }
+  if (g_arch_ok[dev] < 0) return fail(LOWBIT_ERR_DEVICE, "liblowbit_w4 is built for gfx950 only (device %d)", dev);
+  return LOWBIT_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool fits_int(int64_t v) { return v >= 0 && v <= INT_MAX; }
+
+// the reference's check() (csrc/w4_gemv.cu:312-325), minus the tensor-metadata part
+int check_common(const void* x, const void* w, const void* s, const void* y, int64_t M, int64_t N, int64_t K,
+                 int64_t group) {
+  if (!x || !w || !s || !y) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (group <= 0) return fail(LOWBIT_ERR_GROUP, "group size must be positive");
+  if (group % 32 || K % group || K <= 0)
+    return fail(LOWBIT_ERR_GROUP, "K must be a multiple of the group size, itself a multiple of 32");
+  if (N < 1 || !fits_int(N) || !fits_int(K) || !fits_int(M))
+    return fail(LOWBIT_ERR_SHAPE, "shape mismatch");
+  if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned for the 128-bit loads");
+  return LOWBIT_OK;
+}
+
+int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+              int version, int rows_per_wave, void* stream, void* ev0, void* ev1) {
+  if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
+  if (M < 1 || M > 8)
+    return fail(LOWBIT_ERR_ROWS, "the GEMV kernels take 1..8 rows; use the dequantize + matmul path above that");
+  if (!((version >= 1 && version <= 4) || version == 6)) return fail(LOWBIT_ERR_VERSION, "version is 1..4 or 6");
+  if (version == 6 && (K % 128 || group % 128))
+    return fail(LOWBIT_ERR_LAYOUT, "v6 needs K and the group size to be multiples of 128");
+  if (!(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4))
+    return fail(LOWBIT_ERR_TUNING, "rows_per_warp is 0 (auto), 1, 2 or 4");
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev0),
+             static_cast<hipEvent_t>(ev1)};
+  hipError_t e = version == 6 ? gemv_mfma_layout_launch(a, rows_per_wave)
+                              : gemv_rowmajor_launch(a, rows_per_wave, version >= 3);
+  return hip_status(e, "w4_gemv");
+}
+
+int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+              int row_tiles, void* stream, void* ev0, void* ev1) {
+  if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
+  if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the MFMA kernel takes 1..64 rows");
+  if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "v5 needs K and the group size to be multiples of 128");
+  if (!(row_tiles == 0 || row_tiles == 1 || row_tiles == 2 || row_tiles == 4))
+    return fail(LOWBIT_ERR_TUNING, "row_tiles must be 1, 2 or 4");
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev0),
+             static_cast<hipEvent_t>(ev1)};
+  return hip_status(gemm_mfma_launch(a, row_tiles), "w4_gemm_mfma");
+}
+
+}  // namespace
+}  // namespace lowbit
+
+using namespace lowbit;
+
+extern "C" {
+
+const char* lowbit_last_error(void) { return error_buffer(); }
+
+const char* lowbit_strerror(int status) {
+  switch (status) {
+    case LOWBIT_OK: return "ok";
+    case LOWBIT_ERR_ARG: return "invalid argument";
+    case LOWBIT_ERR_GROUP: return "invalid group size";
+    case LOWBIT_ERR_SHAPE: return "shape mismatch";
+    case LOWBIT_ERR_ALIGN: return "misaligned pointer";
+    case LOWBIT_ERR_ROWS: return "row count out of range";
+    case LOWBIT_ERR_VERSION: return "unknown kernel version";
+    case LOWBIT_ERR_LAYOUT: return "layout needs K and G multiples of 128";
+    case LOWBIT_ERR_TUNING: return "invalid tuning knob";
+    case LOWBIT_ERR_HIP: return "HIP error";
+    case LOWBIT_ERR_DEVICE: return "unsupported device";
+    default: return "unknown status";
+  }
+}
+
+const char* lowbit_version(void) { return "lowbit_w4 0.1 gfx950"; }
+
+int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+                   int version, int rows_per_wave, void* stream) {
+  return gemv_impl(x, w, s, y, M, N, K, group, version, rows_per_wave, stream, nullptr, nullptr);
+}
+
+int lowbit_w4_gemv_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                         int64_t group, int version, int rows_per_wave, void* stream, void* start_event,
+                         void* stop_event) {
+  if (!start_event || !stop_event) return fail(LOWBIT_ERR_ARG, "timing events must not be null");
+  return gemv_impl(x, w, s, y, M, N, K, group, version, rows_per_wave, stream, start_event, stop_event);
+}
+
+int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                        int64_t group, int row_tiles, void* stream) {
+  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream, nullptr, nullptr);
+}
+
+int lowbit_w4_gemm_mfma_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                              int64_t group, int row_tiles, void* stream, void* start_event, void* stop_event) {
+  if (!start_event || !stop_event) return fail(LOWBIT_ERR_ARG, "timing events must not be null");
+  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream, start_event, stop_event);
+}
+
+int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_t K, int64_t group, int mfma_layout,
+                      void* stream) {
+  if (!w || !s || !out) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (group <= 0) return fail(LOWBIT_ERR_GROUP, "w [N,K/2], scales [N,K/G], positive group size");
+  if (group % 32 || K % group || K <= 0 || N < 1 || !fits_int(N) || !fits_int(K))
+    return fail(LOWBIT_ERR_SHAPE, "shape mismatch");
+  if (!aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "packed weights must be contiguous and 16-byte aligned");
+  if (!aligned16(out)) return fail(LOWBIT_ERR_ALIGN, "the output must be 16-byte aligned");
+  if (mfma_layout && (K % 128 || group % 128))
+    return fail(LOWBIT_ERR_LAYOUT, "the v5 layout needs K and group % 128 == 0");
+  if (int rc = check_device()) return rc;
+  return hip_status(dequant_launch(static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(out),
+                                   (int)N, (int)K, (int)group, mfma_layout != 0, static_cast<hipStream_t>(stream)),
+                    "w4_dequant");
+}
+
+int lowbit_w4_quantize(const void* w, int w_dtype, void* packed, void* scales, int64_t N, int64_t K, int64_t group,
+                       const float* clip_grid, int n_clip, void* stream) {
+  if (!w || !packed || !scales) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (w_dtype < LOWBIT_DTYPE_F32 || w_dtype > LOWBIT_DTYPE_BF16) return fail(LOWBIT_ERR_ARG, "unknown weight dtype");
+  if (group <= 0 || group % 32 || K <= 0 || K % group)
+    return fail(LOWBIT_ERR_GROUP, "K=%lld must be a multiple of the group size %lld, itself a multiple of 32",
+                (long long)K, (long long)group);
+  if (group > 1024) return fail(LOWBIT_ERR_GROUP, "the GPU quantizer takes group sizes up to 1024");
+  if (N < 1 || !fits_int(N) || !fits_int(K)) return fail(LOWBIT_ERR_SHAPE, "shape mismatch");
+  if (n_clip < 0 || n_clip > kMaxClip || (n_clip > 0 && !clip_grid))
+    return fail(LOWBIT_ERR_ARG, "clip grid must hold 0..%d values", kMaxClip);
+  if (int rc = check_device()) return rc;
+  ClipGrid grid;
+  std::memset(&grid, 0, sizeof(grid));
+  grid.n = n_clip;
+  for (int i = 0; i < n_clip; ++i) grid.a[i] = clip_grid[i];
+  return hip_status(quantize_launch(w, w_dtype, static_cast<uint8_t*>(packed), static_cast<f16*>(scales), (int)N, (int)K,
+                                    (int)group, grid, static_cast<hipStream_t>(stream)),
+                    "w4_quantize");
+}
+
+int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int layout, void* stream) {
+  if (!src || !dst) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (src == dst) return fail(LOWBIT_ERR_ARG, "dst must not alias src");
+  if (layout != LOWBIT_LAYOUT_V3 && layout != LOWBIT_LAYOUT_MFMA)
+    return fail(LOWBIT_ERR_ARG, "device relayout targets the v3 or the MFMA layout");
+  if (N < 1 || K <= 0 || K % 32 || !fits_int(N) || !fits_int(K)) return fail(LOWBIT_ERR_SHAPE, "shape mismatch");
+  if (layout == LOWBIT_LAYOUT_MFMA && K % 128)
+    return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K to be a multiple of 128");
+  if (!aligned16(src) || !aligned16(dst)) return fail(LOWBIT_ERR_ALIGN, "packed weights must be 16-byte aligned");
+  if (int rc = check_device()) return rc;
+  return hip_status(relayout_launch(static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), (int)N, (int)K,
+                                    layout == LOWBIT_LAYOUT_MFMA, static_cast<hipStream_t>(stream)),
+                    "w4_relayout");
+}
+
+}  // extern "C"

@@ -1,0 +1,117 @@
+// Device-side building blocks shared by the gfx950 W4A16 kernels: vector types, the exact nibble decode, wave64
+// reductions (DPP + permlane swaps, no LDS), and the launch helper that can bind timing events to a dispatch.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
+#include <cstdint>
+
+namespace lowbit {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 0x6400 is 1024.0 in fp16, where the mantissa step is exactly 1: (0x6400 | u) reads as 1024 + u for a nibble in
+// bits 0..3, and as 1024 + 16 u for a nibble in bits 4..7.
+constexpr uint32_t kMagic = 0x64006400u;
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+// A 32-bit word in v3 nibble order (slots 0..7 hold k0, k2, k4, k6, k1, k3, k5, k7) -> four fp16 pairs holding the
+// signed values u - 8 exactly: p[0] = (k0, k1), p[1] = (k2, k3), p[2] = (k4, k5), p[3] = (k6, k7).
+// Pairs 1 and 3 sit in bits 4..7 of each half, so (1024 + 16 u) / 16 - 72 = u - 8 (one fused step, exact) saves the
+// shift the low-nibble pairs would need. For a canonical word the same code yields (k0,k4), (k1,k5), (k2,k6), (k3,k7).
+__device__ __forceinline__ void decode_word(uint32_t w, f16x2 p[4]) {
+  const f16x2 m1032 = {(f16)-1032.0f, (f16)-1032.0f};
+  const f16x2 m72 = {(f16)-72.0f, (f16)-72.0f};
+  const f16x2 inv16 = {(f16)0.0625f, (f16)0.0625f};
+  const uint32_t w8 = w >> 8;
+  p[0] = as_f16x2((w & 0x000F000Fu) | kMagic) + m1032;
+  p[1] = as_f16x2((w & 0x00F000F0u) | kMagic) * inv16 + m72;
+  p[2] = as_f16x2((w8 & 0x000F000Fu) | kMagic) + m1032;
+  p[3] = as_f16x2((w8 & 0x00F000F0u) | kMagic) * inv16 + m72;
+}
+
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+constexpr int kQuadSwap1 = 0xB1;       // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kQuadSwap2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kRowHalfMirror = 0x141;  // lane ^ 7 inside 8 lanes
+constexpr int kRowMirror = 0x140;      // lane ^ 15 inside 16 lanes
+
+// sum over the 4 lanes of a quad; every lane of the quad gets the total
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp<kQuadSwap1>(v);
+  v += dpp<kQuadSwap2>(v);
+  return v;
+}
+
+// sum over all 64 lanes of the wave; every lane gets the total
+__device__ __forceinline__ float wave_sum(float v) {
+  v = quad_sum(v);
+  v += dpp<kRowHalfMirror>(v);   // quads are uniform, so lane ^ 7 reaches the other quad of the 8
+  v += dpp<kRowMirror>(v);       // 8-lane groups are uniform, lane ^ 15 reaches the other half of the row
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // (own, lane ^ 16) in some order
+  v = __builtin_bit_cast(float, s16[0]) + __builtin_bit_cast(float, s16[1]);
+  u = __builtin_bit_cast(uint32_t, v);
+  auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);   // (own, lane ^ 32)
+  return __builtin_bit_cast(float, s32[0]) + __builtin_bit_cast(float, s32[1]);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kQuadSwap1>(v));
+  v = fmaxf(v, dpp<kQuadSwap2>(v));
+  v = fmaxf(v, dpp<kRowHalfMirror>(v));
+  v = fmaxf(v, dpp<kRowMirror>(v));
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
+  u = __builtin_bit_cast(uint32_t, v);
+  auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+}
+
+// Raw buffer resource over [base, base + bytes): loads at offsets at or past `bytes` return zeros and touch no
+// memory, so tails and idle lanes need no branch around the load (0x00020000: the gfx9 raw-buffer dword 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kOutOfRange = 0x7FFFFFF0;    // a buffer offset past any resource this library builds
+constexpr int kNonTemporal = 2;            // gfx94x/gfx950 cache policy bit: streamed, no reuse expected
+__device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, kNonTemporal));
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, offset, 0, 0));
+}
+__device__ __forceinline__ uint16_t buffer_load2(__amdgpu_buffer_rsrc_t rsrc, int offset) {
+  return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, offset, 0, 0));
+}
+
+__device__ __forceinline__ u32x4 load_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Launch with or without start/stop events bound to the dispatch packet (hipExtLaunchKernel): with events, their
+// elapsed time is the kernel's own execution time.
+template <typename... KArgs, typename... Args>
+inline hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
+                         hipEvent_t start, hipEvent_t stop, Args... args) {
+  if (start == nullptr && stop == nullptr) {
+    kernel<<<grid, block, shmem, stream>>>(static_cast<KArgs>(args)...);
+  } else {
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)shmem, stream, start, stop, 0, static_cast<KArgs>(args)...);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lowbit

@@ -1,0 +1,315 @@
+// M <= 8 GEMV kernels (no MFMA): y[M, N] = x[M, K] . dequant(W)[N, K]^T, fp16 in/out, fp32 accumulation.
+//
+// gemv_mfma_layout: the deployed decode kernel (the role of the reference's gemv_v6, csrc/w4_gemv.cu:327-391), on the
+//   MFMA layout. A 16-row tile x 128-k chunk is one contiguous 1 KB block; lane l reads the 16 bytes at 16 l, i.e.
+//   row l / 4, k-quarter l % 4 (32 consecutive k), so every wave-load is one fully coalesced 1 KB. Each lane decodes
+//   its 32 nibbles to exact fp16 (u - 8) values, multiplies them with x by v_dot2_f32_f16 into an fp32 partial per
+//   chunk, scales the partial by the group's fp16 scale (fp32 FMA), and keeps going. At the end the 4 lanes of a row
+//   are summed with two quad DPP adds and the waves of the workgroup, which split K, are summed through LDS.
+//   R tiles per wave share each x load. Weights are streamed with non-temporal loads.
+// gemv_rowmajor: the canonical / v3 layouts (reference v2 / v4 roles, csrc/w4_gemv.cu:60-94,150-207), needed when
+//   G or K is not a multiple of 128 and the MFMA layout cannot be used. One wave per R rows; lane l takes the
+//   32-k blocks l, l + 64, ...; wave64 DPP/permlane reduction per row.
+#include <algorithm>
+
+#include "kernels.hpp"
+
+namespace lowbit {
+
+namespace {
+
+// x[m][k0 .. k0 + 32) as 16 fp16 pairs (four 16-byte loads)
+template <int M>
+__device__ __forceinline__ void load_x32(const f16* __restrict__ x, int K, int k0, u32x4 (&xv)[M][4]) {
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[m][j] = load16(x + (size_t)m * K + k0 + 8 * j);
+}
+
+// 32 weights (one 16-byte piece, four v3 words) against x pairs in the same order -> fp32 partial
+__device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
+  float part = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f16x2 p[4];
+    decode_word(wv[j], p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part = dot2(p[e], as_f16x2(xv[j][e]), part);
+  }
+  return part;
+}
+
+}  // namespace
+
+// LDS holds x[M][K] (fp16) and the workgroup's scales [16 R rows][K/G], staged once; the weight pieces stream
+// through a ring of D chunk slots per wave so several 1 KB wave-loads are in flight while earlier ones are decoded.
+// Weight loads go through one buffer resource per tile, so chunks past K and rows past N read as zero without a
+// branch and the compiler can count the loads in flight. When M K is too large for LDS (kLdsX = false) each lane
+// loads its x pairs straight from global memory instead.
+template <int M, int R, bool kLdsX>
+__global__ __launch_bounds__(gemv_max_threads(M, R)) void gemv_mfma_layout(const f16* __restrict__ x,
+                                                                           const uint8_t* __restrict__ w,
+                                                                           const f16* __restrict__ s,
+                                                                           f16* __restrict__ y, int N, int K, int G) {
+  constexpr int D = kGemvRing;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nwaves = blockDim.x >> 6;
+  const int r = lane >> 2, q = lane & 3;
+  const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
+  const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
+  const int t0 = blockIdx.x * R;
+  const int n0 = 16 * t0, nrows = min(16 * R, N - n0);    // rows of this workgroup
+  __amdgpu_buffer_rsrc_t rsrc[R];
+  int off[R], step[R];
+  bool live[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int t = min(t0 + i, ntiles - 1);
+    const int rows = t0 + i < ntiles ? min(16, N - 16 * t) : 0;
+    live[i] = r < rows;
+    rsrc[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
+    off[i] = live[i] ? 64 * r + 16 * q : kOutOfRange;
+    step[i] = live[i] ? rows * 64 : 0;                     // bytes from one chunk to the next inside the tile
+  }
+  // issue the first D chunks of weights before staging x, so both latencies overlap
+  u32x4 ring[D][R];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+#pragma unroll
+    for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(rsrc[i], off[i] + (wave + nwaves * d) * step[i]);
+
+  f16* lds_x = reinterpret_cast<f16*>(smem);
+  f16* lds_s = reinterpret_cast<f16*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
+  if (kLdsX) {
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
+    const int nx = M * K / 8;
+    for (int b = threadIdx.x; b < nx; b += 4 * blockDim.x) {
+      u32x4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = buffer_load16(xr, 16 * (b + u * (int)blockDim.x));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (b + u * (int)blockDim.x < nx) reinterpret_cast<u32x4*>(lds_x)[b + u * blockDim.x] = v[u];
+    }
+  }
+  {
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(nrows * KG * 2));
+    const int ns = nrows * KG;
+    for (int b = threadIdx.x; b < ns; b += 4 * blockDim.x) {
+      uint16_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = buffer_load2(sr, 2 * (b + u * (int)blockDim.x));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (b + u * (int)blockDim.x < ns) reinterpret_cast<uint16_t*>(lds_s)[b + u * blockDim.x] = v[u];
+    }
+  }
+  __syncthreads();
+
+  float acc[R][M];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
+
+  // this wave's chunks are c_j = wave + j * nwaves, j < nj. Full groups of D refill their slot D chunks ahead (past
+  // the end the refill reads zeros); the last partial group drains the ring without refills. Keeping every load
+  // unconditional lets the compiler wait on exactly the slot it needs (vmcnt D - 1 in steady state).
+  const int nj = (KC - wave + nwaves - 1) / nwaves;
+  int sidx[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) sidx[i] = live[i] ? (16 * i + r) * KG : 0;
+  auto consume = [&](const u32x4 (&slot)[R], int c) {
+    u32x4 xv[M][4];
+    if (kLdsX) {
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[m][j] = reinterpret_cast<const u32x4*>(lds_x + (size_t)m * K + 128 * c + 32 * q)[j];
+    } else {
+      load_x32<M>(x, K, 128 * c + 32 * q, xv);
+    }
+    const int g = cpg == 1 ? c : c / cpg;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const float scale = (float)lds_s[sidx[i] + g];
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[i][m] = fmaf(dot32(slot[i], xv[m]), scale, acc[i][m]);
+    }
+  };
+  int j0 = 0;
+  for (; j0 + D <= nj; j0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = wave + (j0 + d) * nwaves;
+      consume(ring[d], c);
+#pragma unroll
+      for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(rsrc[i], off[i] + (c + D * nwaves) * step[i]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d)
+    if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
+  float* red = reinterpret_cast<float*>(smem);              // x and scales are dead after the barrier below
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = quad_sum(acc[i][m]);
+      if (q == 0) red[wave * (R * M * 16) + (i * M + m) * 16 + r] = v;
+    }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * M * 16; idx += blockDim.x) {
+    float v = 0.f;
+    for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * 16) + idx];
+    const int i = idx / (M * 16), m = (idx / 16) % M, rr = idx % 16;
+    const int n = 16 * (t0 + i) + rr;
+    if (n < N) y[(size_t)m * N + n] = (f16)v;
+  }
+}
+
+template <int M, int R, bool kV3>
+__global__ __launch_bounds__(256) void gemv_rowmajor(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                     const f16* __restrict__ s, f16* __restrict__ y, int N, int K,
+                                                     int G) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = (blockIdx.x * (blockDim.x >> 6) + wave) * R;
+  if (n0 >= N) return;
+  const int KB = K >> 5, KG = K / G;
+  float acc[R][M];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
+  for (int b = lane; b < KB; b += 64) {
+    u32x4 wv[R];
+    float sc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int n = min(n0 + i, N - 1);           // rows past N re-read row N - 1; their sums are never stored
+      wv[i] = load_stream(w + (size_t)n * (K / 2) + 16 * b);
+      sc[i] = (float)s[(size_t)n * KG + (32 * b) / G];
+    }
+    u32x4 xv[M][4];
+    load_x32<M>(x, K, 32 * b, xv);
+    if (!kV3) {
+      // canonical words decode to (k0,k4), (k1,k5), (k2,k6), (k3,k7): pair x the same way
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const u32x4 X = xv[m][j];
+          xv[m][j] = u32x4{(X[0] & 0xFFFFu) | (X[2] << 16), (X[0] >> 16) | (X[2] & 0xFFFF0000u),
+                           (X[1] & 0xFFFFu) | (X[3] << 16), (X[1] >> 16) | (X[3] & 0xFFFF0000u)};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[i][m] = fmaf(dot32(wv[i], xv[m]), sc[i], acc[i][m]);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = wave_sum(acc[i][m]);
+      if (lane == 0 && n0 + i < N) y[(size_t)m * N + n0 + i] = (f16)v;
+    }
+}
+
+// ---- host-side launchers ----
+
+namespace {
+
+template <int M, int R>
+hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
+  const int ntiles = (a.N + 15) / 16;
+  dim3 grid((ntiles + R - 1) / R), block(64 * waves);
+  const size_t s_bytes = (size_t)16 * R * (a.K / a.G) * 2, x_bytes = (size_t)M * a.K * 2;
+  const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
+  if (x_bytes + s_bytes <= kGemvLdsX) {
+    const size_t shmem = std::max(x_bytes + s_bytes, red_bytes);
+    return launch(gemv_mfma_layout<M, R, true>, grid, block, shmem, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K,
+                  a.G);
+  }
+  const size_t shmem = std::max(s_bytes, red_bytes);
+  return launch(gemv_mfma_layout<M, R, false>, grid, block, shmem, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K,
+                a.G);
+}
+
+template <int M>
+hipError_t dispatch_mfma_layout(const GemvArgs& a, int R, int waves) {
+  switch (R) {
+    case 1: return launch_mfma_layout<M, 1>(a, waves);
+    case 2: return launch_mfma_layout<M, 2>(a, waves);
+    default: return launch_mfma_layout<M, 4>(a, waves);
+  }
+}
+
+template <int M, int R>
+hipError_t launch_rowmajor(const GemvArgs& a, bool v3) {
+  const int rows = 4 * R;
+  dim3 grid((a.N + rows - 1) / rows), block(256);
+  if (v3) return launch(gemv_rowmajor<M, R, true>, grid, block, 0, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+  return launch(gemv_rowmajor<M, R, false>, grid, block, 0, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+}
+
+template <int M>
+hipError_t dispatch_rowmajor(const GemvArgs& a, int R, bool v3) {
+  switch (R) {
+    case 1: return launch_rowmajor<M, 1>(a, v3);
+    case 2: return launch_rowmajor<M, 2>(a, v3);
+    default: return launch_rowmajor<M, 4>(a, v3);
+  }
+}
+
+}  // namespace
+
+GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
+  GemvPlan p;
+  const int ntiles = (N + 15) / 16, KC = K / 128;
+  p.R = rows_per_wave ? rows_per_wave : (M == 1 && ntiles >= 1024 ? 2 : 1);
+  const int blocks = (ntiles + p.R - 1) / p.R;
+  // enough waves in flight to cover HBM latency: aim at ~2048 waves on the chip, never more waves than chunks
+  const int max_waves = gemv_max_threads(M, p.R) / 64;
+  int waves = 1;
+  while (waves < max_waves && waves * 2 <= KC && (long)blocks * waves < 2048) waves *= 2;
+  p.waves = waves;
+  return p;
+}
+
+int pick_rows_rowmajor(int N, int M) { return N >= 512 ? 4 : (M >= 4 ? 2 : 1); }
+
+hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
+  const GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave);
+  switch (a.M) {
+    case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves);
+    case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves);
+    case 3: return dispatch_mfma_layout<3>(a, p.R, p.waves);
+    case 4: return dispatch_mfma_layout<4>(a, p.R, p.waves);
+    case 5: return dispatch_mfma_layout<5>(a, p.R, p.waves);
+    case 6: return dispatch_mfma_layout<6>(a, p.R, p.waves);
+    case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves);
+    default: return dispatch_mfma_layout<8>(a, p.R, p.waves);
+  }
+}
+
+hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3) {
+  const int R = rows_per_wave ? rows_per_wave : pick_rows_rowmajor(a.N, a.M);
+  switch (a.M) {
+    case 1: return dispatch_rowmajor<1>(a, R, v3);
+    case 2: return dispatch_rowmajor<2>(a, R, v3);
+    case 3: return dispatch_rowmajor<3>(a, R, v3);
+    case 4: return dispatch_rowmajor<4>(a, R, v3);
+    case 5: return dispatch_rowmajor<5>(a, R, v3);
+    case 6: return dispatch_rowmajor<6>(a, R, v3);
+    case 7: return dispatch_rowmajor<7>(a, R, v3);
+    default: return dispatch_rowmajor<8>(a, R, v3);
+  }
+}
+
+}  // namespace lowbit

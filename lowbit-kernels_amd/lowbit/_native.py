@@ -1,0 +1,198 @@
+"""ctypes binding of liblowbit_w4.so (include/lowbit_w4.h) and the torch-facing `ext()` object.
+
+`NativeExt` keeps the three functions of the reference's pybind11 module (csrc/w4_gemv.cu:542-550) with the same
+keyword names and defaults: w4_gemv(x, w, s, group, version, rows_per_warp=0), w4_gemm_tc(x, w, s, group,
+row_tiles=0), w4_dequant(w, s, group, mma_layout=False). Like the reference they check the tensors, allocate the
+output with torch.empty on the input's device, launch on that device's current stream and raise RuntimeError on any
+refusal (the reference's TORCH_CHECK messages). There is no fallback: without the built library every call raises.
+"""
+import ctypes
+import os
+import pathlib
+
+LIB_NAME = "liblowbit_w4.so"
+LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
+
+LAYOUT_CANONICAL, LAYOUT_V3, LAYOUT_MFMA, LAYOUT_NV_MMA = 0, 1, 2, 3
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+_LIB = None
+
+_i64, _int, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+SIGNATURES = {
+    "lowbit_last_error": ([], ctypes.c_char_p),
+    "lowbit_strerror": ([_int], ctypes.c_char_p),
+    "lowbit_version": ([], ctypes.c_char_p),
+    "lowbit_w4_gemv": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp], _int),
+    "lowbit_w4_gemv_timed": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp], _int),
+    "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
+    "lowbit_w4_gemm_mfma_timed": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _vp], _int),
+    "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
+    "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
+    "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
+    "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
+    "lowbit_host_unpack": ([_vp, _vp, _i64, _i64], _int),
+    "lowbit_host_dequantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
+    "lowbit_host_relayout": ([_vp, _vp, _i64, _i64, _int], _int),
+    "lowbit_host_gemv_reference": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64], _int),
+}
+
+
+def lib():
+    """The loaded library (loaded once). Raises RuntimeError if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        path = pathlib.Path(os.environ.get("LOWBIT_LIB", LIB_PATH))
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built: run `python lowbit-kernels_amd/build.py` (hipcc, gfx950)")
+        handle = ctypes.CDLL(str(path))
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes, fn.restype = args, res
+        _LIB = handle
+    return _LIB
+
+
+def check(rc):
+    """Raise RuntimeError with the library's message for a non-zero status."""
+    if rc != 0:
+        l = lib()
+        msg = l.lowbit_last_error().decode() or l.lowbit_strerror(rc).decode()
+        raise RuntimeError(msg)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def np_ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class _DeviceGuard:
+    """Make `device` current for the duration of a call (what the reference's CUDAGuard does), cheaply when it
+    already is."""
+
+    def __init__(self, device):
+        import torch
+        self.torch = torch
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = self.torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            self.torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            self.torch.cuda.set_device(self.prev)
+        return False
+
+
+def _stream(device):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_tensors(x, w, s, group):
+    """The tensor-metadata half of the reference's check() (csrc/w4_gemv.cu:312-325); sizes are checked natively."""
+    import torch
+    if not (x.is_cuda and w.is_cuda and s.is_cuda):
+        raise RuntimeError("tensors must be on the GPU")
+    if w.device != x.device or s.device != x.device:
+        raise RuntimeError("x, w and scales must be on the same GPU")
+    if group <= 0:
+        raise RuntimeError("group size must be positive")
+    if x.dtype != torch.float16 or s.dtype != torch.float16 or w.dtype != torch.uint8:
+        raise RuntimeError("x and scales must be float16, packed weights uint8")
+    if not (x.is_contiguous() and w.is_contiguous() and s.is_contiguous()):
+        raise RuntimeError("tensors must be contiguous")
+    if x.dim() != 2 or w.dim() != 2 or s.dim() != 2:
+        raise RuntimeError("x [M,K], w [N,K/2], scales [N,K/G]")
+    k = x.shape[1]
+    if group % 32 or k % group:
+        raise RuntimeError("K must be a multiple of the group size, itself a multiple of 32")
+    if w.shape[1] * 2 != k or s.shape[0] != w.shape[0] or s.shape[1] != k // group:
+        raise RuntimeError("shape mismatch")
+
+
+class NativeExt:
+    """The reference's extension surface (w4_gemv / w4_gemm_tc / w4_dequant) on the gfx950 library."""
+
+    def __init__(self):
+        self.lib = lib()
+
+    def w4_gemv(self, x, w, s, group, version, rows_per_warp=0):
+        import torch
+        _check_tensors(x, w, s, group)
+        m, n = x.shape[0], w.shape[0]
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_w4_gemv(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group, int(version),
+                                          int(rows_per_warp), _stream(x.device)))
+        return y
+
+    def w4_gemm_tc(self, x, w, s, group, row_tiles=0):
+        import torch
+        _check_tensors(x, w, s, group)
+        m, n = x.shape[0], w.shape[0]
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_w4_gemm_mfma(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group, int(row_tiles),
+                                               _stream(x.device)))
+        return y
+
+    def w4_dequant(self, w, s, group, mma_layout=False):
+        import torch
+        if not (w.is_cuda and s.is_cuda and w.device == s.device):
+            raise RuntimeError("packed weights and scales must be on the same GPU")
+        if w.dtype != torch.uint8 or s.dtype != torch.float16:
+            raise RuntimeError("packed weights uint8, scales float16")
+        if w.dim() != 2 or s.dim() != 2 or group <= 0:
+            raise RuntimeError("w [N,K/2], scales [N,K/G], positive group size")
+        if not (w.is_contiguous() and s.is_contiguous()):
+            raise RuntimeError("packed weights must be contiguous and 16-byte aligned")
+        n, k = w.shape[0], w.shape[1] * 2
+        if group % 32 or k % group or s.shape[0] != n or s.shape[1] != k // group:
+            raise RuntimeError("shape mismatch")
+        out = torch.empty((n, k), dtype=torch.float16, device=w.device)
+        with _DeviceGuard(w.device):
+            check(self.lib.lowbit_w4_dequant(ptr(w), ptr(s), ptr(out), n, k, group, 1 if mma_layout else 0,
+                                             _stream(w.device)))
+        return out
+
+    # ---- beyond the reference's three functions: the device quantizer and relayout ----
+
+    def w4_quantize(self, w, group, clip_grid=None):
+        """Device quantizer: W [N, K] (float32 / float16 / bfloat16, CUDA) -> (packed canonical, scales fp16)."""
+        import torch
+        dtypes = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+        if not w.is_cuda or w.dim() != 2:
+            raise RuntimeError("the GPU quantizer takes a 2-D CUDA tensor")
+        if w.dtype not in dtypes:
+            w = w.float()
+        w = w.contiguous()
+        n, k = w.shape
+        packed = torch.empty((n, k // 2), dtype=torch.uint8, device=w.device)
+        scales = torch.empty((n, k // group if group > 0 else 0), dtype=torch.float16, device=w.device)
+        grid = [float(a) for a in clip_grid] if clip_grid else []
+        arr = (ctypes.c_float * max(1, len(grid)))(*grid)
+        with _DeviceGuard(w.device):
+            check(self.lib.lowbit_w4_quantize(ptr(w), dtypes[w.dtype], ptr(packed), ptr(scales), n, k, group, arr,
+                                              len(grid), _stream(w.device)))
+        return packed, scales
+
+    def w4_relayout(self, packed, layout):
+        """canonical packed [N, K/2] (CUDA) -> a new tensor in LAYOUT_V3 or LAYOUT_MFMA."""
+        import torch
+        if not packed.is_cuda or packed.dtype != torch.uint8 or packed.dim() != 2:
+            raise RuntimeError("packed weights must be a 2-D uint8 CUDA tensor")
+        packed = packed.contiguous()
+        out = torch.empty_like(packed)
+        with _DeviceGuard(packed.device):
+            check(self.lib.lowbit_w4_relayout(ptr(packed), ptr(out), packed.shape[0], packed.shape[1] * 2, int(layout),
+                                              _stream(packed.device)))
+        return out

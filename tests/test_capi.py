@@ -1,0 +1,72 @@
+"""The C ABI on the CPU: the library loads, exports every function include/lowbit_w4.h declares, and refuses bad
+arguments with the reference's messages before it touches any GPU (no kernel runs here)."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from lowbit import _native
+
+HEADER = pathlib.Path(__file__).resolve().parent.parent / "include" / "lowbit_w4.h"
+FAKE = ctypes.c_void_p(4096)          # a 16-byte aligned, non-null address that validation never dereferences
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(lowbit_\w+)\s*\(", text)))
+
+
+def test_header_declares_what_the_binding_binds():
+    assert declared() == sorted(_native.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.lowbit_version().decode().endswith("gfx950")
+
+
+def _msg(rc):
+    assert rc != 0
+    return _native.lib().lowbit_last_error().decode()
+
+
+@pytest.mark.parametrize("call,code,text", [
+    (lambda l: l.lowbit_w4_gemv(None, FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 0, None), 1, "null pointer"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 0, 6, 0, None), 2, "group size must be positive"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 100, 32, 6, 0, None), 2, "multiple of the group size"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 9, 16, 128, 128, 6, 0, None), 5, "1..8 rows"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 128, 5, 0, None), 6, "version is 1..4 or 6"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 96, 32, 6, 0, None), 7, "multiples of 128"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 3, None), 8, "rows_per_warp"),
+    (lambda l: l.lowbit_w4_gemv(ctypes.c_void_p(4098), FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 0, None), 4, "16-byte"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 65, 16, 128, 128, 0, None), 5, "1..64 rows"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 3, None), 8, "row_tiles"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 192, 64, 0, None), 7, "multiples of 128"),
+    (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 128, -1, 0, None), 2, "positive group size"),
+    (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 96, 32, 1, None), 7, "group % 128"),
+    (lambda l: l.lowbit_w4_quantize(FAKE, 0, FAKE, FAKE, 16, 128, 2048, None, 0, None), 2, "multiple of the group"),
+    (lambda l: l.lowbit_w4_quantize(FAKE, 7, FAKE, FAKE, 16, 128, 128, None, 0, None), 1, "dtype"),
+    (lambda l: l.lowbit_w4_relayout(FAKE, FAKE, 16, 128, 2, None), 1, "alias"),
+    (lambda l: l.lowbit_w4_relayout(FAKE, ctypes.c_void_p(8192), 16, 96, 2, None), 7, "multiple of 128"),
+    (lambda l: l.lowbit_w4_gemv_timed(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 0, None, None, None), 1, "events"),
+])
+def test_validation_refuses_before_any_gpu_call(call, code, text):
+    rc = call(_native.lib())
+    assert rc == code
+    assert text in _msg(rc)
+
+
+def test_strerror_names_every_code():
+    lib = _native.lib()
+    names = {lib.lowbit_strerror(c).decode() for c in range(11)}
+    assert len(names) == 11 and "unknown status" not in names
+
+
+def test_check_raises_runtime_error_with_the_message():
+    lib = _native.lib()
+    lib.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 9, 16, 128, 128, 6, 0, None)
+    with pytest.raises(RuntimeError, match="1..8 rows"):
+        _native.check(5)

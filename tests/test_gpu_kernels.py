@@ -1,0 +1,240 @@
+"""GPU parity of every kernel against the CPU oracle, through the same entry points the reference's harness used
+(ops.* and ext().w4_*, i.e. the C ABI). Mirrors the reference's in-benchmark checks (bench/gpu_run.py:144-247):
+bit-exact quantize / relayout / dequant, every GEMV and the MFMA GEMM within max(4 x BLAS, 4 x fp16-output floor,
+3e-3) of fp64 on the same quantized weights, the overflow known answers, the dispatch matrix, side-stream equality,
+refusals, and graph capture."""
+import numpy as np
+import pytest
+import torch
+
+from lowbit import _native, ops
+from oracle import quant_ref as R
+
+pytestmark = pytest.mark.gpu
+
+# (name, K, N): the reference's shapes (bench/gpu_run.py:24-31) plus the k/v shapes of the BASELINE sweep
+SHAPES = [("qwen0.5b.q_proj", 896, 896), ("qwen0.5b.kv_proj", 896, 128), ("qwen0.5b.gate_up", 896, 4864),
+          ("qwen1.5b.kv", 1536, 256), ("qwen3b.q_proj", 2048, 2048), ("qwen3b.down", 11008, 2048)]
+EDGE = [("tiny", 128, 1), ("odd_n", 256, 1001), ("odd_n2", 384, 37)]
+GROUP = 128
+
+
+def make_weight(k, n, seed, group=GROUP, layouts=None, sd=1.0):
+    g = torch.Generator().manual_seed(seed)
+    wf = torch.randn(n, k, generator=g) * sd
+    packed, scales = R.quantize_w4(wf.numpy(), group)
+    wq = ops.W4Weight(packed, scales, group, layouts)
+    ref_w = torch.from_numpy(R.dequantize_w4(packed, scales, group)).double().cuda()
+    return wq, ref_w, packed, scales, g
+
+
+def rel(y, ref):
+    return ((y.double() - ref).abs().max() / ref.pow(2).mean().sqrt()).item()
+
+
+def bound(x, ref_w, ref):
+    """max(4 x BLAS error, 4 x fp16-output floor, 3e-3), the reference's acceptance rule (bench/gpu_run.py:229-245)."""
+    scale = ref.pow(2).mean().sqrt().item()
+    blas = (torch.nn.functional.linear(x, ref_w.half()).double() - ref).abs().max().item() / scale
+    floor = (ref.half().double() - ref).abs().max().item() / scale
+    return max(4 * blas, 4 * floor, R.REL_BOUND)
+
+
+# ---------------------------------------------------------------- format kernels, bit for bit
+
+@pytest.mark.parametrize("n,k", [(1, 128), (37, 384), (16, 256), (1001, 256), (4864, 896), (256, 11008)])
+def test_device_relayout_matches_the_oracle(cuda, n, k):
+    rng = np.random.default_rng(n + k)
+    packed, scales = R.quantize_w4(rng.standard_normal((n, k)).astype(np.float32), 128)
+    wq = ops.W4Weight(packed, scales, 128)
+    assert np.array_equal(wq.packed.cpu().numpy(), packed)
+    assert np.array_equal(wq.packed_v3.cpu().numpy(), R.interleave_for_gpu(packed))
+    assert np.array_equal(wq.packed_mma.cpu().numpy(), R.interleave_for_mfma(packed))
+
+
+@pytest.mark.parametrize("n,k,g,sd,dtype", [(64, 512, 128, 0.02, torch.float32), (37, 384, 128, 1.0, torch.float32),
+                                            (13, 320, 64, 50.0, torch.float32), (9, 96, 32, 1e-4, torch.float32),
+                                            (24, 1024, 256, 0.02, torch.float32), (300, 2048, 128, 0.02, torch.float16),
+                                            (40, 768, 128, 3.0, torch.bfloat16), (5, 2048, 1024, 0.02, torch.float32)])
+def test_gpu_quantizer_is_bit_exact(cuda, n, k, g, sd, dtype):
+    gen = torch.Generator().manual_seed(n * k)
+    w = (torch.randn(n, k, generator=gen) * sd).to(dtype)
+    w[1 % n, :g] = 0
+    packed, scales = ops.quantize_w4_gpu(w.cuda(), g)
+    p_ref, s_ref = R.quantize_w4(w.float().numpy(), g)
+    assert np.array_equal(packed.cpu().numpy(), p_ref)
+    assert np.array_equal(scales.cpu().numpy().view(np.uint16), s_ref.view(np.uint16))
+    # a CPU input goes through in row blocks and gives the same bits
+    packed2, scales2 = ops.quantize_w4_gpu(w, g, rows_per_pass=7)
+    assert torch.equal(packed2, packed) and torch.equal(scales2, scales)
+
+
+def test_gpu_clip_search_agrees_with_the_oracle(cuda):
+    gen = torch.Generator().manual_seed(5)
+    w = torch.randn(512, 2048, generator=gen) * 0.02
+    packed, scales = ops.quantize_w4_gpu(w.cuda(), 128, R.CLIP_GRID)
+    p_ref, s_ref, idx, errs = R.quantize_w4_clip(w.numpy(), 128, R.CLIP_GRID)
+    s_gpu = scales.cpu().numpy()
+    same = s_gpu.view(np.uint16) == s_ref.view(np.uint16)
+    # the fp32 sums run in a different order: a different pick is allowed only on a near-tie
+    g = w.numpy().reshape(512, 16, 128).astype(np.float64)
+    q_gpu = R.unpack_w4(packed.cpu().numpy()).reshape(512, 16, 128).astype(np.float64)
+    e_gpu = ((q_gpu * s_gpu.astype(np.float64)[..., None] - g) ** 2).sum(-1)
+    e_best = errs.min(0).astype(np.float64)
+    assert np.all(e_gpu[~same] <= e_best[~same] * (1 + 1e-5))
+    assert same.mean() > 0.999
+    # where the scale agrees, the packed nibbles agree
+    rows = same.all(1)
+    assert np.array_equal(packed.cpu().numpy()[rows], p_ref[rows])
+
+
+@pytest.mark.parametrize("n,k,g", [(16, 256, 128), (37, 384, 128), (1001, 256, 128), (13, 320, 64), (9, 96, 32),
+                                   (24, 1024, 256), (4864, 896, 128)])
+def test_dequant_is_bit_exact_on_both_layouts(cuda, n, k, g):
+    rng = np.random.default_rng(n * 7 + k)
+    packed, scales = R.quantize_w4(rng.standard_normal((n, k)).astype(np.float32), g)
+    want = R.dequantize_w4_f16(packed, scales, g).view(np.uint16)
+    wq = ops.W4Weight(packed, scales, g)
+    assert np.array_equal(ops.dequant(wq, "canonical").cpu().numpy().view(np.uint16), want)
+    if wq.packed_mma is not None:
+        assert np.array_equal(ops.dequant(wq, "mma").cpu().numpy().view(np.uint16), want)
+    assert np.array_equal(ops.dequantize_w4_gpu(wq.packed, wq.scales, g).cpu().numpy().view(np.uint16), want)
+
+
+def test_dequant_rounds_once_at_extreme_scales(cuda):
+    """Subnormal and near-overflow fp16 results: the product must be rounded exactly once."""
+    rng = np.random.default_rng(3)
+    n, k = 8, 256
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = np.array([2.0 ** -24, 6.0e-8, 3.1e-5, 6.1e-5, 0.0123, 1.0, 4000.0, 8188.0], np.float16)[:, None]
+    scales = np.repeat(scales, k // 128, 1)
+    want = R.dequantize_w4_f16(packed, scales, 128).view(np.uint16)
+    wq = ops.W4Weight(packed, scales, 128)
+    assert np.array_equal(ops.dequant(wq, "canonical").cpu().numpy().view(np.uint16), want)
+    assert np.array_equal(ops.dequant(wq, "mma").cpu().numpy().view(np.uint16), want)
+
+
+def test_golden_fixtures_on_the_gpu(cuda):
+    golden = np.load(__import__("pathlib").Path(__file__).resolve().parent / "golden" / "w4_golden.npz")
+    for case in sorted({f[:-5] for f in golden.files if f.endswith("_meta")}):
+        n, k, g, m, seed = (int(v) for v in golden[f"{case}_meta"])
+        packed, scales = ops.quantize_w4_gpu(torch.from_numpy(golden[f"{case}_w"]).cuda(), g)
+        assert np.array_equal(packed.cpu().numpy(), golden[f"{case}_packed"]), case
+        wq = ops.W4Weight(packed, scales, g)
+        assert np.array_equal(ops.dequant(wq).cpu().numpy().view(np.uint16), golden[f"{case}_dequant16"].view(np.uint16))
+        x = torch.from_numpy(golden[f"{case}_x"]).cuda()
+        ref = torch.from_numpy(golden[f"{case}_y64"]).cuda()
+        y = ops.linear(x, wq)
+        assert rel(y, ref) <= R.REL_BOUND, case
+        if wq.packed_mma is not None:
+            assert np.array_equal(wq.packed_mma.cpu().numpy(), golden[f"{case}_mfma"]), case
+
+
+# ---------------------------------------------------------------- GEMV / GEMM accuracy
+
+@pytest.mark.parametrize("name,k,n", SHAPES + EDGE)
+def test_every_kernel_against_fp64(cuda, name, k, n):
+    wq, ref_w, *_ , gen = make_weight(k, n, k * 7 + n)
+    for m in list(range(1, 9)) + [12, 16, 33, 64]:
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        ref = x.double() @ ref_w.T
+        lim = bound(x, ref_w, ref)
+        versions = [1, 2, 3, 4, 5, 6] if m <= 8 else [5]
+        for v in versions:
+            for rpw in ((0, 1, 2, 4) if v in (4, 5, 6) else (0,)):
+                e = rel(ops.gemv(x, wq, v, rpw), ref)
+                assert e <= lim, (name, m, v, rpw, e, lim)
+
+
+@pytest.mark.parametrize("k,n,g", [(96, 200, 32), (320, 130, 64), (512, 4096, 256), (1024, 3072, 128)])
+def test_group_sizes(cuda, k, n, g):
+    wq, ref_w, *_, gen = make_weight(k, n, k + n + g, group=g)
+    for m in (1, 3, 8):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        ref = x.double() @ ref_w.T
+        for v in (2, 4) + ((5, 6) if wq.packed_mma is not None else ()):
+            assert rel(ops.gemv(x, wq, v), ref) <= bound(x, ref_w, ref), (k, n, g, m, v)
+
+
+def test_overflow_case_is_exact_for_every_kernel(cuda):
+    c = R.OVERFLOW_CASE
+    wq = ops.W4Weight(np.full((c["n"], c["k"] // 2), c["byte"], np.uint8), np.full((c["n"], 1), c["scale"], np.float16), c["k"])
+    for xv, want in c["answers"]:
+        for m in (1, 4, 16):
+            x = torch.full((m, c["k"]), xv, dtype=torch.half, device="cuda")
+            for v in ((1, 2, 3, 4, 5, 6) if m <= 8 else (5,)):
+                y = ops.gemv(x, wq, v).float()
+                assert bool(torch.isfinite(y).all()) and float((y - want).abs().max()) <= c["tol"], (xv, m, v)
+
+
+# ---------------------------------------------------------------- the dispatch matrix (bench/gpu_run.py:162-198)
+
+def test_dispatch_matrix(cuda):
+    cases = [("mma_only_g128", 1024, 3072, 128, ("mma",)), ("mma_only_narrow", 1536, 1000, 128, ("mma",)),
+             ("canonical_g32", 96, 200, 32, None), ("canonical_g64", 320, 130, 64, None), ("mma_g256", 512, 4096, 256, ("mma",))]
+    worst = 0.0
+    for name, k, n, g, layouts in cases:
+        wq, ref_w, *_, gen = make_weight(k, n, k + n + g, group=g, layouts=layouts)
+        for m in (1, 2, 8, 9, 17, 31, 32, 33, 63, 64, 65, 130):
+            x = torch.randn(m, k, generator=gen).half().cuda()
+            e = rel(ops.linear(x, wq), x.double() @ ref_w.T)
+            worst = max(worst, e)
+            assert e <= R.REL_BOUND, (name, m, ops.auto_version(m, wq), e)
+    wq = ops.W4Weight.from_float(torch.randn(256, 512))
+    x = torch.randn(9, 512).half().cuda()
+    assert bool(torch.isfinite(ops.linear(x, wq, max_gemv_rows=16, version=6)).all())      # v6 takes 8: falls back
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y_side = ops.linear(x[:1], wq)
+    s.synchronize()
+    assert torch.equal(y_side, ops.linear(x[:1], wq))
+    for bad in (lambda: ops.ext().w4_dequant(wq.packed, wq.scales.cpu(), 128),           # CPU scales
+                lambda: ops.ext().w4_gemv(x[:1], wq.packed, wq.scales, 0, 1, 0),          # group 0
+                lambda: ops.ext().w4_gemv(x, wq.packed, wq.scales, 128, 1, 0),            # 9 rows into a GEMV
+                lambda: ops.ext().w4_gemm_tc(torch.zeros(65, 512, dtype=torch.half, device="cuda"), wq.packed_mma,
+                                             wq.scales, 128)):                            # 65 rows into v5
+        with pytest.raises(RuntimeError):
+            bad()
+
+
+def test_graph_capture_replays_match_eager(cuda):
+    """Each path captured in a hipGraph (torch.cuda.CUDAGraph), replayed several times with eager work between."""
+    wq, ref_w, *_, gen = make_weight(2048, 1536, 77, layouts=("mma",))
+    for m in (1, 16, 48, 200):
+        x = torch.randn(m, 2048, generator=gen).half().cuda()
+        eager = ops.linear(x, wq)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            ops.linear(x, wq)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = ops.linear(x, wq)
+        for _ in range(3):
+            x.mul_(1.0)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), m
+            ops.linear(x, wq)
+
+
+def test_timed_entry_point_matches_and_times(cuda):
+    lib = _native.lib()
+    wq, ref_w, *_, gen = make_weight(2048, 2048, 9, layouts=("mma",))
+    x = torch.randn(1, 2048, generator=gen).half().cuda()
+    y = torch.empty(1, 2048, dtype=torch.half, device="cuda")
+    hip = __import__("ctypes").CDLL("libamdhip64.so")
+    ev = [__import__("ctypes").c_void_p() for _ in range(2)]
+    for e in ev:
+        assert hip.hipEventCreate(__import__("ctypes").byref(e)) == 0
+    stream = __import__("ctypes").c_void_p(torch.cuda.current_stream().cuda_stream)
+    _native.check(lib.lowbit_w4_gemv_timed(_native.ptr(x), _native.ptr(wq.packed_mma), _native.ptr(wq.scales),
+                                           _native.ptr(y), 1, 2048, 2048, 128, 6, 0, stream, ev[0], ev[1]))
+    assert hip.hipEventSynchronize(ev[1]) == 0
+    ms = __import__("ctypes").c_float()
+    assert hip.hipEventElapsedTime(__import__("ctypes").byref(ms), ev[0], ev[1]) == 0
+    assert 0 < ms.value < 10
+    assert torch.equal(y, ops.gemv(x, wq, 6))
+    for e in ev:
+        hip.hipEventDestroy(e)
