@@ -1,5 +1,5 @@
 // Device-side building blocks shared by the gfx950 W4A16 kernels: vector types, the exact nibble decode, wave64
-// reductions (DPP + permlane swaps, no LDS), and the launch helper that can bind timing events to a dispatch.
+// reductions (DPP + readlane, no LDS), and the launch helper that can bind timing events to a dispatch.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <hip/hip_ext.h>
@@ -53,17 +53,24 @@ __device__ __forceinline__ float quad_sum(float v) {
   return v;
 }
 
-// sum over all 64 lanes of the wave; every lane gets the total
-__device__ __forceinline__ float wave_sum(float v) {
+// sum over the 16 lanes of each row; every lane of the row gets the row's total
+__device__ __forceinline__ float row_sum(float v) {
   v = quad_sum(v);
   v += dpp<kRowHalfMirror>(v);   // quads are uniform, so lane ^ 7 reaches the other quad of the 8
   v += dpp<kRowMirror>(v);       // 8-lane groups are uniform, lane ^ 15 reaches the other half of the row
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);   // (own, lane ^ 16) in some order
-  v = __builtin_bit_cast(float, s16[0]) + __builtin_bit_cast(float, s16[1]);
-  u = __builtin_bit_cast(uint32_t, v);
-  auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);   // (own, lane ^ 32)
-  return __builtin_bit_cast(float, s32[0]) + __builtin_bit_cast(float, s32[1]);
+  return v;
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// sum over all 64 lanes (all lanes must be active); the result is wave-uniform. The four rows are combined through
+// v_readlane in a fixed order, so the sum is deterministic. (permlane16/32_swap with both operands the same value is
+// miscompiled by this toolchain -- both results are taken from one register -- so it is not used for this.)
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum(v);
+  return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -71,12 +78,7 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kQuadSwap2>(v));
   v = fmaxf(v, dpp<kRowHalfMirror>(v));
   v = fmaxf(v, dpp<kRowMirror>(v));
-  uint32_t u = __builtin_bit_cast(uint32_t, v);
-  auto s16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  v = fmaxf(__builtin_bit_cast(float, s16[0]), __builtin_bit_cast(float, s16[1]));
-  u = __builtin_bit_cast(uint32_t, v);
-  auto s32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, s32[0]), __builtin_bit_cast(float, s32[1]));
+  return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 
 // Raw buffer resource over [base, base + bytes): loads at offsets at or past `bytes` return zeros and touch no

@@ -9,7 +9,7 @@
 //   R tiles per wave share each x load. Weights are streamed with non-temporal loads.
 // gemv_rowmajor: the canonical / v3 layouts (reference v2 / v4 roles, csrc/w4_gemv.cu:60-94,150-207), needed when
 //   G or K is not a multiple of 128 and the MFMA layout cannot be used. One wave per R rows; lane l takes the
-//   32-k blocks l, l + 64, ...; wave64 DPP/permlane reduction per row.
+//   32-k blocks l, l + 64, ...; wave64 DPP + readlane reduction per row.
 #include <algorithm>
 
 #include "kernels.hpp"
