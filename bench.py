@@ -13,13 +13,13 @@ Infinity Cache. The K timed steps run as one hipGraph replay (torch.cuda.CUDAGra
 
 value = algorithmic bytes moved per step (int4 weights + fp16 scales + x + y, reference bench/gpu_run.py:255,267)
 x K / elapsed, in GB/s: whole-job throughput including the per-kernel launch gap of the graph.
-roofline = the GEMV kernel alone: the same bytes / its own duration, timed by HIP events bound to each dispatch
-(lowbit_w4_gemv_timed), over K further eager steps on the launch stream; peak = 8 TB/s (MI355X HBM3E).
+roofline = the GEMV kernel: the timed graph holds only its launches, so its average launch duration is elapsed /
+(14 K) and achieved = the same bytes / that time; peak = 8 TB/s (MI355X HBM3E). per_shape: each distinct (K, N) alone,
+per call in a graph over >= 1 GiB of copies.
 cpu_baseline = the reference's CPU path (oracle: dequantize to fp16, then torch.nn.functional.linear on the host) on a
 bounded sample of the same steps.
 """
 import argparse
-import ctypes
 import json
 import os
 import pathlib
@@ -34,6 +34,10 @@ for p in (ROOT / "lowbit-kernels_amd", ROOT):
 GROUP = 128
 CLIP_GRID = tuple(round(1.0 - 0.025 * i, 3) for i in range(11))       # reference bench/e2e.py:30
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per GEMV launch of this workload, measured: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
+# `bench.py --pmc-workload` (20 eager steps), each scaled by what the counter reads for a 1 GiB elementwise copy in the
+# same run (FETCH x2.0, WRITE x1.0); 1.03x the algorithmic bytes. Re-measure when the kernel changes.
+TRAFFIC_PER_LAUNCH = 4712920
 MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
 
 
@@ -61,38 +65,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 BLAS step")
+    ap.add_argument("--no-detail", action="store_true", help="skip the per-shape timings")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
     ap.add_argument("--sweep", choices=["skinny"], default=None)
     ap.add_argument("--out", default=None)
     return ap.parse_args()
-
-
-class HipEvents:
-    """hipEvent_t pairs through libamdhip64 (the events lowbit_w4_gemv_timed binds to a dispatch)."""
-
-    def __init__(self, n):
-        self.hip = ctypes.CDLL("libamdhip64.so")
-        self.ev = []
-        for _ in range(2 * n):
-            e = ctypes.c_void_p()
-            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
-                raise RuntimeError("hipEventCreate failed")
-            self.ev.append(e)
-
-    def pair(self, i):
-        return self.ev[2 * i], self.ev[2 * i + 1]
-
-    def elapsed_ms(self, i):
-        a, b = self.pair(i)
-        if self.hip.hipEventSynchronize(b) != 0:
-            raise RuntimeError("hipEventSynchronize failed")
-        ms = ctypes.c_float()
-        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
-            raise RuntimeError("hipEventElapsedTime failed")
-        return ms.value
-
-    def close(self):
-        for e in self.ev:
-            self.hip.hipEventDestroy(e)
 
 
 def build_pool(torch, ops, projs, gib=1.0, fp16=False, seed=0):
@@ -145,20 +123,68 @@ def cpu_baseline(projs, host, xs, budget_s=15.0):
             "ms_per_step": round(1000 * el / steps, 3)}
 
 
+def graph_time_us(torch, fn, iters, reps=3):
+    """Per-call time of fn(i) for i < iters captured as one hipGraph (best of reps replays after one untimed)."""
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = 1e30
+    for _ in range(reps):
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1000 / iters)
+    del g
+    return best
+
+
+def shape_detail(torch, ops, projs, pool, xs):
+    """Per distinct (K, N): M=1 ops.linear per call in a hipGraph over >= 1 GiB of copies of that layer."""
+    out = {}
+    seen = set()
+    for name, k, n in projs:
+        if (k, n) in seen:
+            continue
+        seen.add((k, n))
+        wq0 = pool[0][name]
+        copies = int(-(-2 ** 30 // w4_bytes(k, n)))
+        cl = []
+        for _ in range(copies):
+            c = ops.W4Weight.__new__(ops.W4Weight)
+            c.__dict__.update(wq0.__dict__)
+            c.packed_mma = wq0.packed_mma.clone()
+            c.scales = wq0.scales.clone()
+            cl.append(c)
+        x = xs[name]
+        us = graph_time_us(torch, lambda i: ops.linear(x, cl[i % copies]), max(400, copies))
+        out[f"{k}x{n}"] = {"us_per_call": round(us, 2), "GBps": round(alg_bytes(k, n) / (us * 1e-6) / 1e9, 1),
+                           "pct_of_8TBps": round(100 * alg_bytes(k, n) / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 1),
+                           "copies": copies}
+        del cl
+        torch.cuda.empty_cache()
+    return out
+
+
 def contract(a):
     import torch
-    from lowbit import _native, ops
+    from lowbit import ops
     from oracle import quant_ref as R
 
     torch.cuda.set_device(0)
-    dev = torch.device("cuda", 0)
     projs = step_projections()
     step_bytes = sum(alg_bytes(k, n) for _, k, n in projs)
     pool, pool16, host, copies = build_pool(torch, ops, projs, fp16=not a.no_fp16)
     gen = torch.Generator(device="cuda").manual_seed(1)
     xs = {name: torch.randn(1, k, generator=gen, device="cuda").half() for name, k, n in projs}
 
-    # parity spot check before timing: every projection of copy 0 against the oracle's fp64 GEMV
+    # parity check before timing: every projection of copy 0 against the oracle's fp64 GEMV on the host copy
     for name, k, n in projs:
         packed, scales = host[0][name]
         ref = R.gemv_reference(xs[name].double().cpu().numpy(), packed, scales, GROUP)
@@ -175,7 +201,7 @@ def contract(a):
         step(i)
     torch.cuda.synchronize()
 
-    # the K timed steps as one graph replay
+    # the K timed steps: one graph replay between two synchronizations
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -195,28 +221,8 @@ def contract(a):
     torch.cuda.synchronize()
     elapsed_ms = e0.elapsed_time(e1)
     del graph
-
-    # kernel-only durations: events bound to each GEMV dispatch, on the launch stream
-    lib = _native.lib()
-    ev = HipEvents(len(projs))
-    stream = torch.cuda.current_stream()
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    ys = {name: torch.empty(1, n, dtype=torch.float16, device=dev) for name, k, n in projs}
-    per = {name: [] for name, _, _ in projs}
-    for i in range(a.steps):
-        layer = pool[i % copies]
-        for j, (name, k, n) in enumerate(projs):
-            wq = layer[name]
-            e_start, e_stop = ev.pair(j)
-            _native.check(lib.lowbit_w4_gemv_timed(_native.ptr(xs[name]), _native.ptr(wq.packed_mma),
-                                                   _native.ptr(wq.scales), _native.ptr(ys[name]), 1, n, k, GROUP, 6, 0,
-                                                   sp, e_start, e_stop))
-        for j, (name, k, n) in enumerate(projs):
-            per[name].append(ev.elapsed_ms(j))
-    ev.close()
-    kernel_ms = sum(sum(v) for v in per.values())
-    launches = sum(len(v) for v in per.values())
-    achieved = step_bytes * a.steps / (kernel_ms / 1e3) / 1e9
+    launches = len(projs) * a.steps
+    value = step_bytes * a.steps / (elapsed_ms / 1e3) / 1e9
 
     # fp16 BLAS on the same cold rotation (dequantized weights), one graph of K steps
     fp16 = None
@@ -225,32 +231,12 @@ def contract(a):
             layer = pool16[i % copies]
             for name, k, n in projs:
                 torch.nn.functional.linear(xs[name], layer[name])
-        step16(0)
-        torch.cuda.synchronize()
-        g16 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g16):
-            for i in range(a.steps):
-                step16(i)
-        g16.replay()
-        torch.cuda.synchronize()
-        e0.record()
-        g16.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        fp16 = e0.elapsed_time(e1) / a.steps
-        del g16
-
-    detail = {}
-    for name, k, n in projs:
-        shape = name.split(".", 1)[1]
-        if shape in ("v", "up"):
-            continue                                       # same shapes as k and gate
-        us = 1000 * sum(per[name]) / len(per[name])
-        detail[f"{name}({k}x{n})"] = {"kernel_us": round(us, 2), "GBps": round(alg_bytes(k, n) / (us * 1e-6) / 1e9, 1)}
+        fp16 = graph_time_us(torch, step16, a.steps, reps=1) / 1000
+    detail = None if a.no_detail else shape_detail(torch, ops, projs, pool, xs)
 
     line = {
         "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1; us/call M=1..64 vs hipBLASLt fp16",
-        "value": round(step_bytes * a.steps / (elapsed_ms / 1e3) / 1e9, 2),
+        "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -265,14 +251,16 @@ def contract(a):
         "config": {"workload": "BASELINE configs[1]: M=1 GEMV over the 7 projections of one Qwen2.5-1.5B and one "
                                "Qwen2.5-3B decoder layer per step (14 launches), hipGraph replay",
                    "step_bytes": step_bytes, "M": 1, "group": GROUP, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "lowbit::gemv_mfma_layout<1,1,true>", "kernel_avg_us": round(1000 * kernel_ms / launches, 3),
-                     "launches": launches},
+        # the timed graph holds only the M=1 GEMV kernel, so its average launch duration is elapsed / launches
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_PER_LAUNCH,
+                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true>",
+                     "kernel_avg_us": round(1000 * elapsed_ms / launches, 3), "launches": launches,
+                     "bytes_per_launch_avg": step_bytes // len(projs)},
         "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,
         "speedup_vs_fp16_blas": round(fp16 / (elapsed_ms / a.steps), 3) if fp16 else None,
         "blas_backend": str(torch.backends.cuda.preferred_blas_library()),
-        "detail": detail,
+        "per_shape": detail,
     }
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(projs, host, xs)
@@ -332,6 +320,30 @@ def sweep_skinny(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+def pmc_workload(a):
+    """For rocprofv3 --pmc: one elementwise copy of exactly 1 GiB (read 1 GiB, write 1 GiB: the calibration of
+    FETCH_SIZE / WRITE_SIZE), then a.steps eager steps of the contract workload (14 GEMV launches each)."""
+    import torch
+    from lowbit import ops
+    torch.cuda.set_device(0)
+    src = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    projs = step_projections()
+    pool, _, _, copies = build_pool(torch, ops, projs)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    xs = {name: torch.randn(1, k, generator=gen, device="cuda").half() for name, k, n in projs}
+    for i in range(a.steps):
+        layer = pool[i % copies]
+        for name, k, n in projs:
+            ops.linear(xs[name], layer[name])
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_workload": True, "steps": a.steps, "launches_per_step": len(projs),
+                      "step_bytes": sum(alg_bytes(k, n) for _, k, n in projs)}), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -341,7 +353,9 @@ def main():
     if int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU only; launch it without torch.distributed.run", file=sys.stderr)
         sys.exit(2)
-    if a.sweep == "skinny":
+    if a.pmc_workload:
+        pmc_workload(a)
+    elif a.sweep == "skinny":
         sweep_skinny(a)
     else:
         contract(a)

@@ -52,6 +52,12 @@ const char* lowbit_strerror(int status);
 /* Library version string. */
 const char* lowbit_version(void);
 
+/* Process-wide launch-shape override of the M <= 8 GEMV on the MFMA layout, for tuning sweeps: waves per workgroup
+ * (0 = automatic, else 1, 2, 4, 8 or 16; clamped to what the register budget allows) and chunk slots in flight per
+ * wave (0 = automatic, 4 or 8; 8 is used only for M <= 2). Affects later launches only. No counterpart in the
+ * reference (its launch shapes were compile-time template choices). */
+int lowbit_set_launch_override(int waves_per_group, int ring);
+
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
  * Replaces the reference's w4_gemv (csrc/w4_gemv.cu:454-484) and, through it, ops.gemv(version in 1..4, 6)
  * (lowbit/ops.py:67-78). version 1 or 2: w in the canonical layout; 3 or 4: v3 layout; 6: the MFMA layout (needs
@@ -100,16 +106,6 @@ int lowbit_host_relayout(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K,
 /* quant.gemv_reference (lowbit/quant.py:81-84): y float64 [M, N] = x float64 [M, K] . dequant(W)^T. */
 int lowbit_host_gemv_reference(const double* x, const uint8_t* packed, const uint16_t* scales, double* y, int64_t M,
                                int64_t N, int64_t K, int64_t group);
-
-/* ---- timing support for the benchmark ----
- * Same as lowbit_w4_gemv / lowbit_w4_gemm_mfma, but the launch carries start/stop hipEvent_t handles bound to the
- * kernel dispatch itself (hipExtLaunchKernel), so their elapsed time is the kernel's own duration, without the
- * queue gap in front of it. No counterpart in the reference (its harness timed CUDA-graph replays). */
-int lowbit_w4_gemv_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                         int64_t group, int version, int rows_per_wave, void* stream, void* start_event,
-                         void* stop_event);
-int lowbit_w4_gemm_mfma_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                              int64_t group, int row_tiles, void* stream, void* start_event, void* stop_event);
 
 #ifdef __cplusplus
 }

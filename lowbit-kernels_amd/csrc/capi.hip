@@ -1,6 +1,7 @@
 // The C ABI (include/lowbit_w4.h): argument validation with the reference's messages, then dispatch to the kernels.
 // The validation mirrors the reference's check() / TORCH_CHECKs (csrc/w4_gemv.cu:312-325,454-540); checks that need
 // tensor metadata (device, dtype, contiguity, dims) are done by the Python layer, which owns the tensors.
+#include <atomic>
 #include <climits>
 #include <cstring>
 
@@ -37,6 +38,8 @@ int check_device() {
   return LOWBIT_OK;
 }
 
+std::atomic<int> g_override_waves{0}, g_override_ring{0};
+
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
   return ok();
@@ -59,7 +62,7 @@ int check_common(const void* x, const void* w, const void* s, const void* y, int
 }
 
 int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
-              int version, int rows_per_wave, void* stream, void* ev0, void* ev1) {
+              int version, int rows_per_wave, void* stream) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 8)
     return fail(LOWBIT_ERR_ROWS, "the GEMV kernels take 1..8 rows; use the dequantize + matmul path above that");
@@ -70,15 +73,14 @@ int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
     return fail(LOWBIT_ERR_TUNING, "rows_per_warp is 0 (auto), 1, 2 or 4");
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
-             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev0),
-             static_cast<hipEvent_t>(ev1)};
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
   hipError_t e = version == 6 ? gemv_mfma_layout_launch(a, rows_per_wave)
                               : gemv_rowmajor_launch(a, rows_per_wave, version >= 3);
   return hip_status(e, "w4_gemv");
 }
 
 int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
-              int row_tiles, void* stream, void* ev0, void* ev1) {
+              int row_tiles, void* stream) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the MFMA kernel takes 1..64 rows");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "v5 needs K and the group size to be multiples of 128");
@@ -86,12 +88,19 @@ int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
     return fail(LOWBIT_ERR_TUNING, "row_tiles must be 1, 2 or 4");
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
-             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev0),
-             static_cast<hipEvent_t>(ev1)};
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
   return hip_status(gemm_mfma_launch(a, row_tiles), "w4_gemm_mfma");
 }
 
 }  // namespace
+
+GemvOverride gemv_override() {
+  GemvOverride o;
+  o.waves = g_override_waves.load(std::memory_order_relaxed);
+  o.ring = g_override_ring.load(std::memory_order_relaxed);
+  return o;
+}
+
 }  // namespace lowbit
 
 using namespace lowbit;
@@ -119,27 +128,24 @@ const char* lowbit_strerror(int status) {
 
 const char* lowbit_version(void) { return "lowbit_w4 0.1 gfx950"; }
 
-int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
-                   int version, int rows_per_wave, void* stream) {
-  return gemv_impl(x, w, s, y, M, N, K, group, version, rows_per_wave, stream, nullptr, nullptr);
+int lowbit_set_launch_override(int waves_per_group, int ring) {
+  if (!(waves_per_group == 0 || waves_per_group == 1 || waves_per_group == 2 || waves_per_group == 4 ||
+        waves_per_group == 8 || waves_per_group == 16))
+    return fail(LOWBIT_ERR_TUNING, "waves_per_group is 0 (auto), 1, 2, 4, 8 or 16");
+  if (!(ring == 0 || ring == 4 || ring == 8)) return fail(LOWBIT_ERR_TUNING, "ring is 0 (auto), 4 or 8");
+  g_override_waves.store(waves_per_group, std::memory_order_relaxed);
+  g_override_ring.store(ring, std::memory_order_relaxed);
+  return ok();
 }
 
-int lowbit_w4_gemv_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                         int64_t group, int version, int rows_per_wave, void* stream, void* start_event,
-                         void* stop_event) {
-  if (!start_event || !stop_event) return fail(LOWBIT_ERR_ARG, "timing events must not be null");
-  return gemv_impl(x, w, s, y, M, N, K, group, version, rows_per_wave, stream, start_event, stop_event);
+int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+                   int version, int rows_per_wave, void* stream) {
+  return gemv_impl(x, w, s, y, M, N, K, group, version, rows_per_wave, stream);
 }
 
 int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
                         int64_t group, int row_tiles, void* stream) {
-  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream, nullptr, nullptr);
-}
-
-int lowbit_w4_gemm_mfma_timed(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                              int64_t group, int row_tiles, void* stream, void* start_event, void* stop_event) {
-  if (!start_event || !stop_event) return fail(LOWBIT_ERR_ARG, "timing events must not be null");
-  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream, start_event, stop_event);
+  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream);
 }
 
 int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_t K, int64_t group, int mfma_layout,

@@ -1,8 +1,7 @@
 // Device-side building blocks shared by the gfx950 W4A16 kernels: vector types, the exact nibble decode, wave64
-// reductions (DPP + readlane, no LDS), and the launch helper that can bind timing events to a dispatch.
+// reductions (DPP + readlane, no LDS), buffer-resource loads and the launch helper.
 #pragma once
 #include <hip/hip_runtime.h>
-#include <hip/hip_ext.h>
 #include <cstdint>
 
 namespace lowbit {
@@ -36,6 +35,19 @@ __device__ __forceinline__ void decode_word(uint32_t w, f16x2 p[4]) {
 }
 
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// Subnormal decode for dot products: a nibble alone in the mantissa of an fp16 half (exponent 0) is the subnormal
+// u * 2^-24 (bits 0..3) or u * 2^-20 (bits 4..7), which v_dot2_f32_f16 multiplies exactly (fp16 denormals are on).
+// For a v3 word: lo[0] = (k0, k1), lo[1] = (k4, k5) scaled 2^-24; hi[0] = (k2, k3), hi[1] = (k6, k7) scaled 2^-20.
+// The offset 8 is removed by subtracting the same dot2 sequence run on nibbles 8 (see the GEMV), so runs of zero
+// weights cancel exactly.
+__device__ __forceinline__ void decode_word_subnormal(uint32_t w, f16x2 lo[2], f16x2 hi[2]) {
+  const uint32_t w8 = w >> 8;
+  lo[0] = as_f16x2(w & 0x000F000Fu);
+  hi[0] = as_f16x2(w & 0x00F000F0u);
+  lo[1] = as_f16x2(w8 & 0x000F000Fu);
+  hi[1] = as_f16x2(w8 & 0x00F000F0u);
+}
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp(float v) {
@@ -103,16 +115,11 @@ __device__ __forceinline__ u32x4 load_stream(const void* p) {
 }
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-// Launch with or without start/stop events bound to the dispatch packet (hipExtLaunchKernel): with events, their
-// elapsed time is the kernel's own execution time.
+// Launch on `stream` and report the launch status.
 template <typename... KArgs, typename... Args>
 inline hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t stream,
-                         hipEvent_t start, hipEvent_t stop, Args... args) {
-  if (start == nullptr && stop == nullptr) {
-    kernel<<<grid, block, shmem, stream>>>(static_cast<KArgs>(args)...);
-  } else {
-    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)shmem, stream, start, stop, 0, static_cast<KArgs>(args)...);
-  }
+                         Args... args) {
+  kernel<<<grid, block, shmem, stream>>>(static_cast<KArgs>(args)...);
   return hipGetLastError();
 }
 

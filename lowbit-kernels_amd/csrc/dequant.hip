@@ -73,15 +73,15 @@ __global__ __launch_bounds__(256) void relayout_kernel(const uint8_t* __restrict
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st) {
   const size_t total = (size_t)N * (K / 32);
   dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (mfma) return launch(dequant_kernel<true>, grid, block, 0, st, nullptr, nullptr, w, s, out, N, K, G);
-  return launch(dequant_kernel<false>, grid, block, 0, st, nullptr, nullptr, w, s, out, N, K, G);
+  if (mfma) return launch(dequant_kernel<true>, grid, block, 0, st, w, s, out, N, K, G);
+  return launch(dequant_kernel<false>, grid, block, 0, st, w, s, out, N, K, G);
 }
 
 hipError_t relayout_launch(const uint8_t* src, uint8_t* dst, int N, int K, bool mfma, hipStream_t st) {
   const size_t total = (size_t)N * (K / 32);
   dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (mfma) return launch(relayout_kernel<true>, grid, block, 0, st, nullptr, nullptr, src, dst, N, K);
-  return launch(relayout_kernel<false>, grid, block, 0, st, nullptr, nullptr, src, dst, N, K);
+  if (mfma) return launch(relayout_kernel<true>, grid, block, 0, st, src, dst, N, K);
+  return launch(relayout_kernel<false>, grid, block, 0, st, src, dst, N, K);
 }
 
 }  // namespace lowbit

@@ -127,7 +127,7 @@ hipError_t launch_gemm(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
   dim3 grid((ntiles + RT - 1) / RT), block(64 * waves);
   const size_t shmem = waves > 1 ? (size_t)waves * RT * MT * 64 * 4 * sizeof(float) : 0;
-  return launch(gemm_mfma<MT, RT>, grid, block, shmem, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G);
+  return launch(gemm_mfma<MT, RT>, grid, block, shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G);
 }
 
 template <int MT>

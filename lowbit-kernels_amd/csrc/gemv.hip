@@ -42,17 +42,19 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 
 }  // namespace
 
-// LDS holds x[M][K] (fp16) and the workgroup's scales [16 R rows][K/G], staged once; the weight pieces stream
-// through a ring of D chunk slots per wave so several 1 KB wave-loads are in flight while earlier ones are decoded.
-// Weight loads go through one buffer resource per tile, so chunks past K and rows past N read as zero without a
-// branch and the compiler can count the loads in flight. When M K is too large for LDS (kLdsX = false) each lane
-// loads its x pairs straight from global memory instead.
-template <int M, int R, bool kLdsX>
-__global__ __launch_bounds__(gemv_max_threads(M, R)) void gemv_mfma_layout(const f16* __restrict__ x,
+// One memory round trip before the first chunk is decoded. The prologue first requests x (the workgroup stages all
+// of x[M][K] into LDS) and the workgroup's fp16 scales, then the weight pieces of each wave's first D chunks. Load
+// counters retire in order, so staging x waits only for the x and scale loads while the weights are still in flight;
+// one barrier later every wave decodes as its weights arrive. Later chunks stream through the same D slots, each
+// refilled as soon as it is consumed. Weight loads use one buffer resource per tile: chunks past K and rows past N
+// read as zero without a branch, so the compiler waits on exactly the slot it needs. When M K is too large for LDS
+// (kLdsX = false) each lane loads its x pairs from global memory and decodes exactly.
+template <int M, int R, int D, bool kLdsX>
+__global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
                                                                            f16* __restrict__ y, int N, int K, int G) {
-  constexpr int D = kGemvRing;
+  constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -62,51 +64,89 @@ __global__ __launch_bounds__(gemv_max_threads(M, R)) void gemv_mfma_layout(const
   const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
   const int t0 = blockIdx.x * R;
   const int n0 = 16 * t0, nrows = min(16 * R, N - n0);    // rows of this workgroup
-  __amdgpu_buffer_rsrc_t rsrc[R];
-  int off[R], step[R];
-  bool live[R];
+  // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16
+  f16* lds_x = reinterpret_cast<f16*>(smem);
+  float* lds_xs = reinterpret_cast<float*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
+  f16* lds_s = reinterpret_cast<f16*>(smem + (kLdsX ? (size_t)M * K * 2 + (size_t)M * (K / 32) * 8 : 0));
+
+  // 1. x and scale requests
+  const int nb = M * (K / 32), ns = nrows * KG;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(ns * 2));
+  u32x4 xst[XB][4];
+  if (kLdsX) {
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      if (b < nb) {                                         // only threads that own a block issue its loads
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xst[u][j] = buffer_load16(xr, 64 * b + 16 * j);
+      }
+    }
+  }
+  uint16_t sst[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = (int)threadIdx.x + u * (int)blockDim.x;
+    if (i < ns) sst[u] = buffer_load2(sr, 2 * i);
+  }
+
+  // 2. the weight ring
+  __amdgpu_buffer_rsrc_t wr[R];
+  int woff[R], wstep[R], srow[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int t = min(t0 + i, ntiles - 1);
     const int rows = t0 + i < ntiles ? min(16, N - 16 * t) : 0;
-    live[i] = r < rows;
-    rsrc[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
-    off[i] = live[i] ? 64 * r + 16 * q : kOutOfRange;
-    step[i] = live[i] ? rows * 64 : 0;                     // bytes from one chunk to the next inside the tile
+    const bool live = r < rows;
+    wr[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
+    woff[i] = live ? 64 * r + 16 * q : kOutOfRange;
+    wstep[i] = live ? rows * 64 : 0;                       // bytes from one chunk to the next inside the tile
+    srow[i] = live ? (16 * i + r) * KG : 0;                // this lane's row in the staged scales
   }
-  // issue the first D chunks of weights before staging x, so both latencies overlap
   u32x4 ring[D][R];
 #pragma unroll
   for (int d = 0; d < D; ++d)
 #pragma unroll
-    for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(rsrc[i], off[i] + (wave + nwaves * d) * step[i]);
+    for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (wave + nwaves * d) * wstep[i]);
 
-  f16* lds_x = reinterpret_cast<f16*>(smem);
-  f16* lds_s = reinterpret_cast<f16*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
+  // 3. stage x with the decode's own dot2 sequence run on zero weights (every nibble 8), over the lo positions
+  //    (k % 8 in 0,1,4,5) and the hi positions (2,3,6,7) of each 32-k block: a block of real weights minus these is
+  //    2^-24 sum((u - 8) x) (lo) and 2^-20 sum((u - 8) x) (hi), and exactly 0 where the weights are zero.
+  const f16x2 z8lo = as_f16x2(0x00080008u), z8hi = as_f16x2(0x00800080u);
+  auto stage_block = [&](int b, const u32x4 (&v)[4]) {
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      reinterpret_cast<u32x4*>(lds_x)[4 * b + j] = v[j];
+      lo = dot2(z8lo, as_f16x2(v[j][0]), lo);
+      hi = dot2(z8hi, as_f16x2(v[j][1]), hi);
+      lo = dot2(z8lo, as_f16x2(v[j][2]), lo);
+      hi = dot2(z8hi, as_f16x2(v[j][3]), hi);
+    }
+    lds_xs[2 * b] = lo;
+    lds_xs[2 * b + 1] = hi;
+  };
   if (kLdsX) {
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
-    const int nx = M * K / 8;
-    for (int b = threadIdx.x; b < nx; b += 4 * blockDim.x) {
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      if (b < nb) stage_block(b, xst[u]);
+    }
+    for (int b = (int)threadIdx.x + XB * (int)blockDim.x; b < nb; b += blockDim.x) {   // long x only
       u32x4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = buffer_load16(xr, 16 * (b + u * (int)blockDim.x));
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (b + u * (int)blockDim.x < nx) reinterpret_cast<u32x4*>(lds_x)[b + u * blockDim.x] = v[u];
+      for (int j = 0; j < 4; ++j) v[j] = buffer_load16(xr, 64 * b + 16 * j);
+      stage_block(b, v);
     }
   }
-  {
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(nrows * KG * 2));
-    const int ns = nrows * KG;
-    for (int b = threadIdx.x; b < ns; b += 4 * blockDim.x) {
-      uint16_t v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = buffer_load2(sr, 2 * (b + u * (int)blockDim.x));
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (b + u * (int)blockDim.x < ns) reinterpret_cast<uint16_t*>(lds_s)[b + u * blockDim.x] = v[u];
-    }
+  for (int u = 0; u < 2; ++u) {
+    const int i = (int)threadIdx.x + u * (int)blockDim.x;
+    if (i < ns) reinterpret_cast<uint16_t*>(lds_s)[i] = sst[u];
   }
+  for (int i = (int)threadIdx.x + 2 * (int)blockDim.x; i < ns; i += blockDim.x)
+    reinterpret_cast<uint16_t*>(lds_s)[i] = buffer_load2(sr, 2 * i);
   __syncthreads();
 
   float acc[R][M];
@@ -116,28 +156,55 @@ __global__ __launch_bounds__(gemv_max_threads(M, R)) void gemv_mfma_layout(const
     for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
 
   // this wave's chunks are c_j = wave + j * nwaves, j < nj. Full groups of D refill their slot D chunks ahead (past
-  // the end the refill reads zeros); the last partial group drains the ring without refills. Keeping every load
-  // unconditional lets the compiler wait on exactly the slot it needs (vmcnt D - 1 in steady state).
+  // the end the refill reads zeros); the last partial group drains the ring without refills.
   const int nj = (KC - wave + nwaves - 1) / nwaves;
-  int sidx[R];
-#pragma unroll
-  for (int i = 0; i < R; ++i) sidx[i] = live[i] ? (16 * i + r) * KG : 0;
+  const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
   auto consume = [&](const u32x4 (&slot)[R], int c) {
+    const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
     u32x4 xv[M][4];
     if (kLdsX) {
+      float xs[M][2];
 #pragma unroll
-      for (int m = 0; m < M; ++m)
+      for (int m = 0; m < M; ++m) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xv[m][j] = reinterpret_cast<const u32x4*>(lds_x + (size_t)m * K + 128 * c + 32 * q)[j];
+        const int blk = m * (K / 32) + 4 * c + q;
+        xs[m][0] = lds_xs[2 * blk];
+        xs[m][1] = lds_xs[2 * blk + 1];
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const float scale = (float)lds_s[srow[i] + g];
+        float lo[M], hi[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) lo[m] = hi[m] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f16x2 pl[2], ph[2];
+          decode_word_subnormal(slot[i][j], pl, ph);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            lo[m] = dot2(pl[0], as_f16x2(xv[m][j][0]), lo[m]);
+            hi[m] = dot2(ph[0], as_f16x2(xv[m][j][1]), hi[m]);
+            lo[m] = dot2(pl[1], as_f16x2(xv[m][j][2]), lo[m]);
+            hi[m] = dot2(ph[1], as_f16x2(xv[m][j][3]), hi[m]);
+          }
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          // sum((u - 8) x) over the lane's 32 k (exactly 0 for zero weights), then the group scale
+          const float part = fmaf(lo[m] - xs[m][0], 16777216.0f, (hi[m] - xs[m][1]) * 1048576.0f);
+          acc[i][m] = fmaf(part, scale, acc[i][m]);
+        }
+      }
     } else {
       load_x32<M>(x, K, 128 * c + 32 * q, xv);
-    }
-    const int g = cpg == 1 ? c : c / cpg;
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const float scale = (float)lds_s[sidx[i] + g];
+      for (int i = 0; i < R; ++i) {
+        const float scale = (float)lds_s[srow[i] + g];
 #pragma unroll
-      for (int m = 0; m < M; ++m) acc[i][m] = fmaf(dot32(slot[i], xv[m]), scale, acc[i][m]);
+        for (int m = 0; m < M; ++m) acc[i][m] = fmaf(dot32(slot[i], xv[m]), scale, acc[i][m]);
+      }
     }
   };
   int j0 = 0;
@@ -147,13 +214,25 @@ __global__ __launch_bounds__(gemv_max_threads(M, R)) void gemv_mfma_layout(const
       const int c = wave + (j0 + d) * nwaves;
       consume(ring[d], c);
 #pragma unroll
-      for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(rsrc[i], off[i] + (c + D * nwaves) * step[i]);
+      for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (c + D * nwaves) * wstep[i]);
     }
   }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d)
     if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
-  float* red = reinterpret_cast<float*>(smem);              // x and scales are dead after the barrier below
+
+  if (nwaves == 1) {                                        // no split of K: the quad sums are the outputs
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float v = quad_sum(acc[i][m]);
+        const int n = 16 * (t0 + i) + r;
+        if (q == 0 && n < N) y[(size_t)m * N + n] = (f16)v;
+      }
+    return;
+  }
+  float* red = reinterpret_cast<float*>(smem);              // x is dead after the barrier below
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < R; ++i)
@@ -225,28 +304,34 @@ __global__ __launch_bounds__(256) void gemv_rowmajor(const f16* __restrict__ x, 
 
 namespace {
 
-template <int M, int R>
+template <int M, int R, int D>
 hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
   dim3 grid((ntiles + R - 1) / R), block(64 * waves);
-  const size_t s_bytes = (size_t)16 * R * (a.K / a.G) * 2, x_bytes = (size_t)M * a.K * 2;
+  const size_t s_bytes = (size_t)16 * R * (a.K / a.G) * 2;
+  const size_t x_bytes = (size_t)M * a.K * 2 + (size_t)M * (a.K / 32) * 8;
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
-  if (x_bytes + s_bytes <= kGemvLdsX) {
-    const size_t shmem = std::max(x_bytes + s_bytes, red_bytes);
-    return launch(gemv_mfma_layout<M, R, true>, grid, block, shmem, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K,
-                  a.G);
-  }
-  const size_t shmem = std::max(s_bytes, red_bytes);
-  return launch(gemv_mfma_layout<M, R, false>, grid, block, shmem, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K,
-                a.G);
+  if (x_bytes + s_bytes <= kGemvLdsX)
+    return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+  return launch(gemv_mfma_layout<M, R, D, false>, grid, block, std::max(s_bytes, red_bytes), a.stream,
+                a.x, a.w, a.s, a.y, a.N, a.K, a.G);
 }
 
 template <int M>
-hipError_t dispatch_mfma_layout(const GemvArgs& a, int R, int waves) {
+hipError_t dispatch_mfma_layout(const GemvArgs& a, int R, int waves, int D) {
+  if constexpr (M <= 2) {
+    if (D > 4) {
+      switch (R) {
+        case 1: return launch_mfma_layout<M, 1, 8>(a, waves);
+        case 2: return launch_mfma_layout<M, 2, 8>(a, waves);
+        default: break;
+      }
+    }
+  }
   switch (R) {
-    case 1: return launch_mfma_layout<M, 1>(a, waves);
-    case 2: return launch_mfma_layout<M, 2>(a, waves);
-    default: return launch_mfma_layout<M, 4>(a, waves);
+    case 1: return launch_mfma_layout<M, 1, 4>(a, waves);
+    case 2: return launch_mfma_layout<M, 2, 4>(a, waves);
+    default: return launch_mfma_layout<M, 4, 4>(a, waves);
   }
 }
 
@@ -254,8 +339,8 @@ template <int M, int R>
 hipError_t launch_rowmajor(const GemvArgs& a, bool v3) {
   const int rows = 4 * R;
   dim3 grid((a.N + rows - 1) / rows), block(256);
-  if (v3) return launch(gemv_rowmajor<M, R, true>, grid, block, 0, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
-  return launch(gemv_rowmajor<M, R, false>, grid, block, 0, a.stream, a.ev0, a.ev1, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+  if (v3) return launch(gemv_rowmajor<M, R, true>, grid, block, 0, a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+  return launch(gemv_rowmajor<M, R, false>, grid, block, 0, a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
 }
 
 template <int M>
@@ -272,13 +357,23 @@ hipError_t dispatch_rowmajor(const GemvArgs& a, int R, bool v3) {
 GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
   GemvPlan p;
   const int ntiles = (N + 15) / 16, KC = K / 128;
-  p.R = rows_per_wave ? rows_per_wave : (M == 1 && ntiles >= 1024 ? 2 : 1);
+  const GemvOverride o = gemv_override();
+  // From the MI355X graph-mode sweep over the Qwen2.5-1.5B/3B and 7B-shaped projections (M = 1): one 16-row tile
+  // per wave always; 8 waves splitting K on narrow layers (16 on long rows), fewer as the tile count grows so that
+  // about 3k waves are in flight; never more waves than 128-k chunks; 4 chunk slots in flight per wave.
+  p.R = rows_per_wave ? rows_per_wave : 1;
   const int blocks = (ntiles + p.R - 1) / p.R;
-  // enough waves in flight to cover HBM latency: aim at ~2048 waves on the chip, never more waves than chunks
-  const int max_waves = gemv_max_threads(M, p.R) / 64;
-  int waves = 1;
-  while (waves < max_waves && waves * 2 <= KC && (long)blocks * waves < 2048) waves *= 2;
-  p.waves = waves;
+  int waves;
+  if (blocks >= 256) {
+    waves = 1;
+    while (waves < 8 && blocks * waves * 2 <= 3072) waves *= 2;
+  } else {
+    waves = KC >= 128 ? 16 : 8;
+  }
+  while (waves > 1 && waves > KC) waves /= 2;
+  if (o.waves > 0) waves = o.waves;
+  p.D = (o.ring > 0 && M <= 2) ? o.ring : 4;
+  p.waves = std::min(waves, gemv_max_threads(M, p.R, p.D) / 64);
   return p;
 }
 
@@ -287,14 +382,14 @@ int pick_rows_rowmajor(int N, int M) { return N >= 512 ? 4 : (M >= 4 ? 2 : 1); }
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
   const GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave);
   switch (a.M) {
-    case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves);
-    case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves);
-    case 3: return dispatch_mfma_layout<3>(a, p.R, p.waves);
-    case 4: return dispatch_mfma_layout<4>(a, p.R, p.waves);
-    case 5: return dispatch_mfma_layout<5>(a, p.R, p.waves);
-    case 6: return dispatch_mfma_layout<6>(a, p.R, p.waves);
-    case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves);
-    default: return dispatch_mfma_layout<8>(a, p.R, p.waves);
+    case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves, p.D);
+    case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves, p.D);
+    case 3: return dispatch_mfma_layout<3>(a, p.R, p.waves, p.D);
+    case 4: return dispatch_mfma_layout<4>(a, p.R, p.waves, p.D);
+    case 5: return dispatch_mfma_layout<5>(a, p.R, p.waves, p.D);
+    case 6: return dispatch_mfma_layout<6>(a, p.R, p.waves, p.D);
+    case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves, p.D);
+    default: return dispatch_mfma_layout<8>(a, p.R, p.waves, p.D);
   }
 }
 

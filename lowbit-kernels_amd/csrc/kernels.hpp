@@ -11,20 +11,28 @@ struct GemvArgs {
   f16* y;
   int M, N, K, G;
   hipStream_t stream;
-  hipEvent_t ev0, ev1;      // optional timing events bound to the dispatch (both null = plain launch)
 };
 
 struct GemvPlan {
   int R = 1;        // 16-row tiles per wave (MFMA layout) or rows per wave (row-major layouts)
   int waves = 1;    // waves per workgroup, splitting K
   int MT = 1;       // 16-column activation tiles (MFMA GEMM)
+  int D = 4;        // chunk slots in flight per wave (M <= 8 GEMV)
 };
 
-// largest workgroup the M=1..8 MFMA-layout GEMV uses, from its register needs (x pairs and R weight pieces)
-constexpr int gemv_max_threads(int M, int R) { return M * R <= 2 ? 1024 : (M * R <= 8 ? 512 : 256); }
+// process-wide launch-shape override for tuning sweeps (lowbit_set_launch_override); 0 = automatic
+struct GemvOverride {
+  int waves = 0;
+  int ring = 0;
+};
+GemvOverride gemv_override();
 
-constexpr int kGemvRing = 4;             // chunk slots in flight per wave in the M <= 8 GEMV
-constexpr size_t kGemvLdsX = 65536;      // x + scales staged in LDS up to this many bytes (default dynamic LDS limit)
+// largest workgroup the M=1..8 MFMA-layout GEMV uses, from its register needs (x pairs, R weight pieces, D slots)
+constexpr int gemv_max_threads(int M, int R, int D = 4) {
+  return (M * R == 1 && D <= 4) ? 1024 : (M * R <= 4 ? 512 : 256);
+}
+
+constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many bytes (the default dynamic LDS limit)
 
 constexpr int kMaxClip = 64;
 struct ClipGrid {

@@ -95,9 +95,9 @@ hipError_t quantize_launch(const void* w, int dtype, uint8_t* packed, f16* scale
   const size_t groups = (size_t)N * (K / G);
   dim3 gr((unsigned)((groups + 3) / 4)), block(256);
   switch (dtype) {
-    case 0: return launch(quantize_kernel<0>, gr, block, 0, st, nullptr, nullptr, w, packed, scales, N, K, G, grid);
-    case 1: return launch(quantize_kernel<1>, gr, block, 0, st, nullptr, nullptr, w, packed, scales, N, K, G, grid);
-    default: return launch(quantize_kernel<2>, gr, block, 0, st, nullptr, nullptr, w, packed, scales, N, K, G, grid);
+    case 0: return launch(quantize_kernel<0>, gr, block, 0, st, w, packed, scales, N, K, G, grid);
+    case 1: return launch(quantize_kernel<1>, gr, block, 0, st, w, packed, scales, N, K, G, grid);
+    default: return launch(quantize_kernel<2>, gr, block, 0, st, w, packed, scales, N, K, G, grid);
   }
 }
 

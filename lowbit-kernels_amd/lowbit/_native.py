@@ -23,10 +23,9 @@ SIGNATURES = {
     "lowbit_last_error": ([], ctypes.c_char_p),
     "lowbit_strerror": ([_int], ctypes.c_char_p),
     "lowbit_version": ([], ctypes.c_char_p),
+    "lowbit_set_launch_override": ([_int, _int], _int),
     "lowbit_w4_gemv": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp], _int),
-    "lowbit_w4_gemv_timed": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp, _vp, _vp], _int),
     "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
-    "lowbit_w4_gemm_mfma_timed": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, _vp], _int),
     "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),

@@ -51,7 +51,8 @@ def _msg(rc):
     (lambda l: l.lowbit_w4_quantize(FAKE, 7, FAKE, FAKE, 16, 128, 128, None, 0, None), 1, "dtype"),
     (lambda l: l.lowbit_w4_relayout(FAKE, FAKE, 16, 128, 2, None), 1, "alias"),
     (lambda l: l.lowbit_w4_relayout(FAKE, ctypes.c_void_p(8192), 16, 96, 2, None), 7, "multiple of 128"),
-    (lambda l: l.lowbit_w4_gemv_timed(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 0, None, None, None), 1, "events"),
+    (lambda l: l.lowbit_set_launch_override(3, 0), 8, "waves_per_group"),
+    (lambda l: l.lowbit_set_launch_override(4, 5), 8, "ring"),
 ])
 def test_validation_refuses_before_any_gpu_call(call, code, text):
     rc = call(_native.lib())
