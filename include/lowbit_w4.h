@@ -22,6 +22,7 @@
 #ifndef LOWBIT_W4_H
 #define LOWBIT_W4_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -52,11 +53,13 @@ const char* lowbit_strerror(int status);
 /* Library version string. */
 const char* lowbit_version(void);
 
-/* Process-wide launch-shape override of the M <= 8 GEMV on the MFMA layout, for tuning sweeps: waves per workgroup
- * (0 = automatic, else 1, 2, 4, 8 or 16; clamped to what the register budget allows) and chunk slots in flight per
- * wave (0 = automatic, 4 or 8; 8 is used only for M <= 2). Affects later launches only. No counterpart in the
- * reference (its launch shapes were compile-time template choices). */
-int lowbit_set_launch_override(int waves_per_group, int ring);
+/* Process-wide launch-shape override of the two MFMA-layout kernels, for tuning sweeps. waves_per_group: the M <= 8
+ * GEMV's waves per workgroup (0 = automatic, else 1, 2, 4, 8 or 16; clamped to what the register budget allows).
+ * ring: chunk slots in flight per wave (0 = automatic, else 2, 3, 4 or 8: the GEMV uses 4 or 8, 8 only for M <= 2;
+ * the MFMA GEMM uses 2, 3 or 4). k_splits: workgroups the MFMA GEMM splits K over (0 = automatic, 1..32; bounded by
+ * the workspace and by K / 256). Affects later launches only. No counterpart in the reference (its launch shapes
+ * were compile-time template choices). */
+int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
  * Replaces the reference's w4_gemv (csrc/w4_gemv.cu:454-484) and, through it, ops.gemv(version in 1..4, 6)
@@ -66,11 +69,20 @@ int lowbit_set_launch_override(int waves_per_group, int ring);
 int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
                    int version, int rows_per_wave, void* stream);
 
+/* Workspace of lowbit_w4_gemm_mfma: LOWBIT_WORKSPACE_COUNTER_BYTES of arrival counters, which must be zero before
+ * the first call and which every call leaves zero, then fp32 partial sums. LOWBIT_WORKSPACE_BYTES lets every shape
+ * with M * N <= 65536 split K the full 32 ways; a smaller workspace splits less. */
+#define LOWBIT_WORKSPACE_COUNTER_BYTES 16384
+#define LOWBIT_WORKSPACE_BYTES (LOWBIT_WORKSPACE_COUNTER_BYTES + (16u << 20))
+
 /* y[M, N] (fp16) = x[M, K] . dequant(W)^T on the MFMA layout with fp16 MFMA (fp32 accumulate), 1 <= M <= 64.
  * Replaces the reference's w4_gemm_tc (csrc/w4_gemv.cu:486-515), i.e. ops.gemv(version 5) (lowbit/ops.py:75-76).
- * row_tiles: 0 = chosen from N and M, else 1, 2 or 4 sixteen-row tiles per wave. */
+ * row_tiles: 0 = automatic, else 1, 2 or 4 sixteen-row tiles per wave. workspace (device memory, 16-byte aligned,
+ * see above; may be NULL): lets narrow N split K across workgroups; the partial sums are added in a fixed order,
+ * so a given shape, workspace size and override give the same bits on every call. Calls that share a workspace must not run concurrently (one stream per workspace). The workspace argument
+ * has no counterpart in the reference, whose extension allocated nothing beyond the output. */
 int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                        int64_t group, int row_tiles, void* stream);
+                        int64_t group, int row_tiles, void* workspace, size_t workspace_bytes, void* stream);
 
 /* out[N, K] (fp16) = (u - 8) * scale rounded once to fp16, from the canonical (mfma_layout = 0) or the MFMA layout
  * (mfma_layout = 1). Both give the same bits. Replaces the reference's w4_dequant (csrc/w4_gemv.cu:517-540), i.e.

@@ -38,7 +38,7 @@ int check_device() {
   return LOWBIT_OK;
 }
 
-std::atomic<int> g_override_waves{0}, g_override_ring{0};
+std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -61,6 +61,16 @@ int check_common(const void* x, const void* w, const void* s, const void* y, int
   return LOWBIT_OK;
 }
 
+// 32-bit buffer offsets bound K and the scale count for the MFMA-layout kernels; the GEMV also stages the scales of
+// its rows in LDS, which bounds K / G
+int check_mfma_layout_limits(int64_t N, int64_t K, int64_t group, bool gemv) {
+  if (K > kMaxK) return fail(LOWBIT_ERR_SHAPE, "K is at most %lld for the MFMA-layout kernels", (long long)kMaxK);
+  if (gemv && K / group > kMaxGroups)
+    return fail(LOWBIT_ERR_GROUP, "K / group is at most %d for the v6 GEMV", kMaxGroups);
+  if (N * (K / group) * 2 > INT_MAX) return fail(LOWBIT_ERR_SHAPE, "N * K / group scales exceed 2^30");
+  return LOWBIT_OK;
+}
+
 int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
               int version, int rows_per_wave, void* stream) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
@@ -69,6 +79,8 @@ int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
   if (!((version >= 1 && version <= 4) || version == 6)) return fail(LOWBIT_ERR_VERSION, "version is 1..4 or 6");
   if (version == 6 && (K % 128 || group % 128))
     return fail(LOWBIT_ERR_LAYOUT, "v6 needs K and the group size to be multiples of 128");
+  if (version == 6)
+    if (int rc = check_mfma_layout_limits(N, K, group, true)) return rc;
   if (!(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4))
     return fail(LOWBIT_ERR_TUNING, "rows_per_warp is 0 (auto), 1, 2 or 4");
   if (int rc = check_device()) return rc;
@@ -80,16 +92,19 @@ int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
 }
 
 int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
-              int row_tiles, void* stream) {
+              int row_tiles, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the MFMA kernel takes 1..64 rows");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "v5 needs K and the group size to be multiples of 128");
+  if (int rc = check_mfma_layout_limits(N, K, group, false)) return rc;
   if (!(row_tiles == 0 || row_tiles == 1 || row_tiles == 2 || row_tiles == 4))
     return fail(LOWBIT_ERR_TUNING, "row_tiles must be 1, 2 or 4");
+  if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
+    return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
              (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
-  return hip_status(gemm_mfma_launch(a, row_tiles), "w4_gemm_mfma");
+  return hip_status(gemm_mfma_launch(a, row_tiles, workspace, workspace_bytes), "w4_gemm_mfma");
 }
 
 }  // namespace
@@ -98,6 +113,7 @@ GemvOverride gemv_override() {
   GemvOverride o;
   o.waves = g_override_waves.load(std::memory_order_relaxed);
   o.ring = g_override_ring.load(std::memory_order_relaxed);
+  o.splits = g_override_splits.load(std::memory_order_relaxed);
   return o;
 }
 
@@ -128,13 +144,16 @@ const char* lowbit_strerror(int status) {
 
 const char* lowbit_version(void) { return "lowbit_w4 0.1 gfx950"; }
 
-int lowbit_set_launch_override(int waves_per_group, int ring) {
+int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
   if (!(waves_per_group == 0 || waves_per_group == 1 || waves_per_group == 2 || waves_per_group == 4 ||
         waves_per_group == 8 || waves_per_group == 16))
     return fail(LOWBIT_ERR_TUNING, "waves_per_group is 0 (auto), 1, 2, 4, 8 or 16");
-  if (!(ring == 0 || ring == 4 || ring == 8)) return fail(LOWBIT_ERR_TUNING, "ring is 0 (auto), 4 or 8");
+  if (!(ring == 0 || ring == 2 || ring == 3 || ring == 4 || ring == 8))
+    return fail(LOWBIT_ERR_TUNING, "ring is 0 (auto), 2, 3, 4 or 8");
+  if (k_splits < 0 || k_splits > kMaxSplits) return fail(LOWBIT_ERR_TUNING, "k_splits is 0 (auto) .. %d", kMaxSplits);
   g_override_waves.store(waves_per_group, std::memory_order_relaxed);
   g_override_ring.store(ring, std::memory_order_relaxed);
+  g_override_splits.store(k_splits, std::memory_order_relaxed);
   return ok();
 }
 
@@ -144,8 +163,8 @@ int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t
 }
 
 int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                        int64_t group, int row_tiles, void* stream) {
-  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, stream);
+                        int64_t group, int row_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+  return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, workspace, workspace_bytes, stream);
 }
 
 int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_t K, int64_t group, int mfma_layout,

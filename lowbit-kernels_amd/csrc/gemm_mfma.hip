@@ -5,163 +5,376 @@
 //   A (16 weight rows x 32 k): row r, 8 consecutive k of quarter q. In the MFMA layout lane l's 16-byte piece of a
 //     1 KB block is exactly row r, k = 128 c + 32 q + [0, 32): word j of it feeds k-step j, so one coalesced 1 KB
 //     wave-load gives the A fragments of four MFMAs with no shuffle.
-//   B (32 k x 16 activation rows): x[16 mt + r][128 c + 32 q + 8 j + 0..7], one 16-byte load per lane and k-step.
+//   B (32 k x 16 activation rows): x[16 mt + r][128 c + 32 q + 8 j + 0..7], 16 bytes read from LDS.
 //   D: lane l holds rows n = 16 t + 4 q + v (v = 0..3) of column m = 16 mt + r.
-// Each lane decodes its words to exact (u - 8) fp16 values and multiplies them by the group's fp16 scale (one
-// rounding: the same fp16 weights the dequant kernel writes), so accumulation across groups stays inside the MFMA
-// accumulators. The waves of a workgroup split the K chunks and are summed through LDS at the end.
+//
+// Decode: a nibble alone in bits 0..3 of an fp16 half is the exact subnormal u 2^-24 (fp16 denormals are on), so a
+// v3 word becomes the eight A values (pairs (k0,k1), (k2,k3), (k4,k5), (k6,k7)) with three shifts and four ANDs, and
+// every product u x 2^-24 is exact in fp32 whatever the magnitude of x. The offset 8 is removed per 128-k chunk by
+// subtracting the same MFMAs run on the constant "all nibbles 8": zero weights give exactly 0, and the rest is
+// sum((u - 8) x) 2^-24 accumulated in fp32. That chunk partial is multiplied by its rows' scales into the running
+// sums (2^24 is put back at the end).
+//
+// Workgroup: 4 x KS waves. Wave w owns RW 16-row tiles (tile-wave w % 4) in K-group w / 4; the K-groups split the
+// workgroup's 128-k chunks round-robin. The 4 waves of a K-group walk the same chunks, so each chunk of x is loaded
+// from memory once per K-group (coalesced, 16 bytes per thread and row piece) and shared through LDS (double buffered,
+// one barrier per step). Each wave keeps D chunks in flight: per slot its tiles' weight pieces and scales and the
+// thread's x pieces, issued together because load counters retire in order. Buffer loads make tails free: rows past
+// N and chunks past the workgroup's range read zeros (and add nothing), activation rows past M read zeros. At the end
+// the K-groups are summed through LDS.
+//
+// Narrow N cannot fill 256 CUs with row groups alone, so K is also split over S workgroups per row group (grid.y)
+// when the caller passes a workspace. Each writes its fp32 partial sums; one thread per workgroup then makes them
+// visible and counts the arrival (release), and the last to arrive (acquire) adds the S partials in split order,
+// writes y and resets the counter to 0. Results do not depend on timing.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace lowbit {
 
-template <int MT, int RT>
-__global__ __launch_bounds__(256) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
-                                                 const f16* __restrict__ s, f16* __restrict__ y, int M, int N, int K,
-                                                 int G) {
-  extern __shared__ float red[];                          // [nwaves][RT][MT][64 lanes][4]
-  const int lane = threadIdx.x & 63, nwaves = blockDim.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+namespace {
+
+constexpr int kW = 4;              // waves per workgroup
+constexpr int kXPitch = 272;       // bytes per staged activation row (256 + 16: conflict-free 16-byte LDS reads)
+constexpr float kTwo24 = 16777216.0f;
+
+template <int kV>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {   // value of lane kV of each quad
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kV | (kV << 2) | (kV << 4) | (kV << 6), 0xF, 0xF, false);
+}
+
+}  // namespace
+
+template <int MT, int RW, int D, int KS>
+__global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                      const f16* __restrict__ s, f16* __restrict__ y, int M, int N,
+                                                      int K, int G, int S, uint32_t* __restrict__ ctr,
+                                                      float* __restrict__ part) {
+  constexpr int T = kW * RW;                               // 16-row tiles per workgroup
+  constexpr int kXBuf = 16 * MT * kXPitch;                 // one staged chunk of x
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_last;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wave >> 2, tw = wave & 3, gt = tid & 255;  // K-group, tile-wave, thread index inside the K-group
   const int r = lane & 15, q = lane >> 4;
   const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
+  const int grp = blockIdx.x, split = blockIdx.y;
+  const int n0 = 16 * T * grp;
+  const int cb = (int)((int64_t)KC * split / S), ce = (int)((int64_t)KC * (split + 1) / S);
+  const int nsteps = (ce - cb + KS - 1) / KS;               // K-group kg takes chunks cb + kg + KS j
   const size_t tile_bytes = (size_t)8 * K;
-  const uint8_t* wp[RT];
-  const f16* sp[RT];
-  int rows[RT];
-  bool live[RT];
+  uint8_t* xbuf = smem + kg * 2 * kXBuf;                    // this K-group's two x buffers
+
+  // per tile: weight resource and offsets, scale offset of this lane's row 4 q + (r & 3)
+  __amdgpu_buffer_rsrc_t wr[RW];
+  int woff[RW], wstep[RW], soff[RW];
 #pragma unroll
-  for (int i = 0; i < RT; ++i) {
-    const int t = blockIdx.x * RT + i;
-    rows[i] = t < ntiles ? min(16, N - 16 * t) : 0;
-    live[i] = r < rows[i];
-    wp[i] = w + (live[i] ? t * tile_bytes + 64 * r + 16 * q : 0);
-    sp[i] = s + (size_t)(live[i] ? 16 * t + r : 0) * KG;
+  for (int i = 0; i < RW; ++i) {
+    const int t = T * grp + tw * RW + i;
+    const int tc = min(t, ntiles - 1);
+    const int rows = t < ntiles ? min(16, N - 16 * t) : 0;
+    wr[i] = make_rsrc(w + tc * tile_bytes, (uint32_t)(rows * (K / 2)));
+    woff[i] = r < rows ? 64 * r + 16 * q : kOutOfRange;
+    wstep[i] = r < rows ? rows * 64 : 0;                    // bytes from one chunk to the next inside the tile
+    const int srow = 16 * t + 4 * q + (r & 3);
+    soff[i] = srow < N ? 2 * srow * KG : kOutOfRange;
   }
-  const f16* xr[MT];
-  bool xlive[MT];
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)N * (uint32_t)KG * 2u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  int xoff[MT];                                              // this thread's x pieces: row gt / 16 + 16 u
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * mt + r;
-    xlive[mt] = m < M;
-    xr[mt] = x + (size_t)(xlive[mt] ? m : 0) * K + 32 * q;
-  }
-  f32x4 acc[RT][MT];
+  for (int u = 0; u < MT; ++u) xoff[u] = (((gt >> 4) + 16 * u) * K + 8 * (gt & 15)) * 2;   // rows >= M: past the end
+
+  u32x4 rw[D][RW], rx[D][MT];
+  uint32_t rs[D][RW];
+  const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
+  auto issue = [&](int d, int step) {
+    const int c = cb + kg + KS * step;
+    const bool live = c < ce;
+    const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
+    for (int i = 0; i < RW; ++i) {
+      rw[d][i] = buffer_load16_nt(wr[i], live ? woff[i] + c * wstep[i] : kOutOfRange);
+      rs[d][i] = buffer_load2(sr, live ? soff[i] + 2 * g : kOutOfRange);
+    }
+#pragma unroll
+    for (int u = 0; u < MT; ++u) rx[d][u] = buffer_load16(xr, live ? xoff[u] + 256 * c : kOutOfRange);
+  };
+  auto stage_x = [&](int d, int b) {                        // x pieces of slot d -> LDS buffer b
+#pragma unroll
+    for (int u = 0; u < MT; ++u)
+      *reinterpret_cast<u32x4*>(xbuf + b * kXBuf + ((gt >> 4) + 16 * u) * kXPitch + 16 * (gt & 15)) = rx[d][u];
+  };
+
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(d, d);
+  stage_x(0, 0);
+  __syncthreads();
+
+  f32x4 acc[RW][MT];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int c = wave; c < KC; c += nwaves) {
-    u32x4 wv[RT];
-    f16x2 sc[RT];
+  const f16x8 a8 = __builtin_bit_cast(f16x8, u32x4{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+  auto consume = [&](int d, int b) {
+    f32x4 pt[RW][MT], xs[MT];
 #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      wv[i] = live[i] ? load_stream(wp[i] + (size_t)c * rows[i] * 64) : u32x4{0, 0, 0, 0};
-      const f16 sv = sp[i][c / cpg];
-      sc[i] = f16x2{sv, sv};
+    for (int mt = 0; mt < MT; ++mt) {
+      xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < RW; ++i) pt[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    u32x4 xv[MT][4];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xv[mt][j] = xlive[mt] ? load16(xr[mt] + 128 * c + 8 * j) : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        f16x2 p[4];
-        decode_word(wv[i][j], p);
-        const f16x8 a = {(f16)0, (f16)0, (f16)0, (f16)0, (f16)0, (f16)0, (f16)0, (f16)0};
-        f16x8 av = a;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f16x2 wsc = p[e] * sc[i];              // exact (u - 8) times the fp16 scale, rounded once
-          av[2 * e] = wsc[0];
-          av[2 * e + 1] = wsc[1];
-        }
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(f16x8, xv[mt][j]), acc[i][mt], 0,
-                                                              0, 0);
-      }
-    }
-  }
-  if (nwaves > 1) {
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        *reinterpret_cast<f32x4*>(red + ((((size_t)wave * RT + i) * MT + mt) * 64 + lane) * 4) = acc[i][mt];
-    __syncthreads();
-    // the waves share the final sums: tile-pair (i, mt) goes to wave (i * MT + mt) % nwaves
-    for (int tp = wave; tp < RT * MT; tp += nwaves) {
-      const int i = tp / MT, mt = tp % MT;
-      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int wv2 = 0; wv2 < nwaves; ++wv2)
-        v += *reinterpret_cast<const f32x4*>(red + ((((size_t)wv2 * RT + i) * MT + mt) * 64 + lane) * 4);
-      const int m = 16 * mt + r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int n = 16 * (blockIdx.x * RT + i) + 4 * q + e;
-        if (m < M && n < N) y[(size_t)m * N + n] = (f16)v[e];
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
+      f16x8 bx[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = 16 * mt + r;
+        bx[mt] = *reinterpret_cast<const f16x8*>(xbuf + b * kXBuf + (16 * mt + r) * kXPitch + 16 * (4 * q + j));
+        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, bx[mt], xs[mt], 0, 0, 0);
+      }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int n = 16 * (blockIdx.x * RT + i) + 4 * q + e;
-          if (m < M && n < N) y[(size_t)m * N + n] = (f16)acc[i][mt][e];
+      for (int i = 0; i < RW; ++i) {
+        const uint32_t wd = rw[d][i][j];
+        const f16x8 a = __builtin_bit_cast(
+            f16x8, u32x4{wd & 0x000F000Fu, (wd >> 4) & 0x000F000Fu, (wd >> 8) & 0x000F000Fu, (wd >> 12) & 0x000F000Fu});
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) pt[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[mt], pt[i][mt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const uint32_t sb = rs[d][i];
+      const float sc[4] = {(float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<0>(sb)),
+                           (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<1>(sb)),
+                           (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<2>(sb)),
+                           (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<3>(sb))};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[i][mt][v] = fmaf(pt[i][mt][v] - xs[mt][v], sc[v], acc[i][mt][v]);
+    }
+  };
+
+  // step j uses ring slot j % D and LDS buffer j % 2; full groups of D refill their slot D steps ahead, the last
+  // partial group drains the ring. After step j the next step's x goes to the other buffer. Every K-group runs the
+  // same number of steps (a step past the group's chunks reads zeros and adds nothing), so the barriers match.
+  int j0 = 0;
+  for (; j0 + D <= nsteps; j0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int j = j0 + d;
+      consume(d, j & 1);
+      issue(d, j + D);
+      if (j + 1 < nsteps) stage_x((d + 1) % D, (j + 1) & 1);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d) {
+    const int j = j0 + d;
+    if (j < nsteps) {
+      consume(d, j & 1);
+      if (j + 1 < nsteps) stage_x(d + 1, (j + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // sum the K-groups through LDS (the x buffers are free after the last barrier); K-group 0 keeps the totals
+  if (KS > 1) {
+    f32x4* red = reinterpret_cast<f32x4*>(smem);            // [KS - 1][4][RW][MT][64]
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[((((kg - 1) * kW + tw) * RW + i) * MT + mt) * 64 + lane] = acc[i][mt];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int g2 = 1; g2 < KS; ++g2)
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[i][mt] += red[((((g2 - 1) * kW + tw) * RW + i) * MT + mt) * 64 + lane];
+    }
+  }
+
+  // epilogue: K-group 0 holds the totals; the lane has rows n .. n + 3 of column m per (tile, column tile). Every
+  // wave stays to the end, so each barrier below sees the whole workgroup.
+  const bool vec = (N & 3) == 0;
+  if (S == 1) {
+    if (kg > 0) return;
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
+        if (m >= M || n >= N) continue;
+        const f32x4 v = acc[i][mt] * kTwo24;
+        f16* dst = y + (size_t)m * N + n;
+        if (vec) {
+          const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
+          *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) dst[e] = (f16)v[e];
         }
       }
+    return;
+  }
+  float* mine = part + (size_t)split * M * N;               // [S][M][N] fp32
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
+      if (kg > 0 || m >= M || n >= N) continue;
+      const f32x4 v = acc[i][mt] * kTwo24;
+      float* dst = mine + (size_t)m * N + n;
+      if (vec) {
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) dst[e] = v[e];
+      }
+    }
+  // the barrier orders every wave's partial stores before thread 0's release; only the last arrival acquires, so the
+  // other workgroups keep their caches
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(ctr + grp, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (uint32_t)(S - 1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (tid == 0) __hip_atomic_store(ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int nrows = min(16 * T, N - n0), nq = (nrows + 3) >> 2;
+  for (int it = tid; it < M * nq; it += 256 * KS) {
+    const int m = it / nq, n = n0 + 4 * (it - m * nq);
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    f16* dst = y + (size_t)m * N + n;
+    if (vec) {
+      for (int sp = 0; sp < S; ++sp) sum += *reinterpret_cast<const f32x4*>(part + ((size_t)sp * M + m) * N + n);
+      const f16x2 lo = {(f16)sum[0], (f16)sum[1]}, hi = {(f16)sum[2], (f16)sum[3]};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+    } else {
+      for (int sp = 0; sp < S; ++sp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) sum[e] += part[((size_t)sp * M + m) * N + n + e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = (f16)sum[e];
+    }
   }
 }
 
 namespace {
 
-template <int MT, int RT>
-hipError_t launch_gemm(const GemvArgs& a, int waves) {
-  const int ntiles = (a.N + 15) / 16;
-  dim3 grid((ntiles + RT - 1) / RT), block(64 * waves);
-  const size_t shmem = waves > 1 ? (size_t)waves * RT * MT * 64 * 4 * sizeof(float) : 0;
-  return launch(gemm_mfma<MT, RT>, grid, block, shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G);
+template <int MT, int RW, int D, int KS>
+hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  if constexpr (!gemm_fits(MT, RW, D, KS)) {
+    return hipErrorInvalidConfiguration;                    // never planned
+  } else {
+    const int ntiles = (a.N + 15) / 16, groups = (ntiles + kW * RW - 1) / (kW * RW);
+    const size_t xbytes = (size_t)KS * 2 * 16 * MT * kXPitch, redbytes = (size_t)(KS - 1) * kW * RW * MT * 1024;
+    const size_t shmem = std::max(xbytes, redbytes);
+    auto kern = gemm_mfma<MT, RW, D, KS>;
+    if (shmem > 65536) {                                     // above the default dynamic LDS limit (gfx950 has 160 KB)
+      static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+      if (attr != hipSuccess) return attr;
+    }
+    return launch(kern, dim3(groups, p.S), dim3(256 * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G,
+                  p.S, ctr, part);
+  }
+}
+
+template <int MT, int RW, int D>
+hipError_t dispatch_kgroups(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  switch (p.waves / kW) {
+    case 1: return launch_gemm<MT, RW, D, 1>(a, p, ctr, part);
+    case 2: return launch_gemm<MT, RW, D, 2>(a, p, ctr, part);
+    default: return launch_gemm<MT, RW, D, 4>(a, p, ctr, part);
+  }
+}
+
+template <int MT, int RW>
+hipError_t dispatch_ring(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  switch (p.D) {
+    case 2: return dispatch_kgroups<MT, RW, 2>(a, p, ctr, part);
+    case 3: return dispatch_kgroups<MT, RW, 3>(a, p, ctr, part);
+    default: return dispatch_kgroups<MT, RW, 4>(a, p, ctr, part);
+  }
 }
 
 template <int MT>
-hipError_t dispatch_gemm(const GemvArgs& a, int RT, int waves) {
-  switch (RT) {
-    case 1: return launch_gemm<MT, 1>(a, waves);
-    case 2: return launch_gemm<MT, 2>(a, waves);
-    default: return launch_gemm<MT, 4>(a, waves);
+hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  switch (p.R) {
+    case 1: return dispatch_ring<MT, 1>(a, p, ctr, part);
+    default: return dispatch_ring<MT, 2>(a, p, ctr, part);
   }
 }
 
 }  // namespace
 
-GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles) {
+// Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
+// tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
+// N); K-groups per workgroup until about kGemmTargetWaves waves run; a 3-slot ring for M <= 16 with up to two K-groups,
+// else 2 slots.
+GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
-  const int MT = (M + 15) / 16, ntiles = (N + 15) / 16, KC = K / 128;
-  int RT = row_tiles ? row_tiles : (M <= 16 ? 1 : 2);
-  if (MT >= 3 && RT > 2) RT = 2;                 // accumulators: 4 RT MT floats per lane
-  p.R = RT;
-  const int blocks = (ntiles + RT - 1) / RT;
-  int waves = 1;
-  while (waves < 4 && waves * 2 <= KC && (long)blocks * waves < 2048) waves *= 2;
-  p.waves = waves;
-  p.MT = MT;
+  const GemvOverride o = gemv_override();
+  const int ntiles = (N + 15) / 16, KC = K / 128;
+  p.MT = (M + 15) / 16;
+  p.R = row_tiles >= 2 ? 2 : 1;
+  const int groups = (ntiles + kW * p.R - 1) / (kW * p.R);
+  const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
+  int S = 1;
+  if (o.splits > 0) {
+    S = o.splits;
+  } else if (part_bytes > 0) {
+    while (S < kMaxSplits && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 2 * S) S *= 2;
+  }
+  S = std::min(S, std::max(1, KC));
+  while (S > 1 && (size_t)S * M * N * sizeof(float) > part_bytes) --S;
+  if (groups > (int)(kCounterBytes / 4)) S = 1;
+  int ks = 1;
+  if (o.waves >= 4) {
+    ks = o.waves / 4;
+  } else {
+    while (ks < 4 && (long)groups * S * kW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
+  }
+  while (ks > 1 && ks * S > KC) ks /= 2;
+  p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);
+  while (!gemm_fits(p.MT, p.R, p.D, ks)) {                  // fewer K-groups, then fewer slots, then fewer tiles
+    if (ks > 1) ks /= 2;
+    else if (p.D > 2) --p.D;
+    else p.R = 1;
+  }
+  p.waves = kW * ks;
+  p.S = std::max(S, 1);
   return p;
 }
 
-hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles) {
-  const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles);
+hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
+  const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
+  uint32_t* ctr = static_cast<uint32_t*>(workspace);
+  float* part = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes) : nullptr;
   switch (p.MT) {
-    case 1: return dispatch_gemm<1>(a, p.R, p.waves);
-    case 2: return dispatch_gemm<2>(a, p.R, p.waves);
-    case 3: return dispatch_gemm<3>(a, p.R, p.waves);
-    default: return dispatch_gemm<4>(a, p.R, p.waves);
+    case 1: return dispatch_rows<1>(a, p, ctr, part);
+    case 2: return dispatch_rows<2>(a, p, ctr, part);
+    case 3: return dispatch_rows<3>(a, p, ctr, part);
+    default: return dispatch_rows<4>(a, p, ctr, part);
   }
 }
 

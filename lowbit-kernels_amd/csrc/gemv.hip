@@ -372,7 +372,7 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
   }
   while (waves > 1 && waves > KC) waves /= 2;
   if (o.waves > 0) waves = o.waves;
-  p.D = (o.ring > 0 && M <= 2) ? o.ring : 4;
+  p.D = ((o.ring == 4 || o.ring == 8) && M <= 2) ? o.ring : 4;
   p.waves = std::min(waves, gemv_max_threads(M, p.R, p.D) / 64);
   return p;
 }

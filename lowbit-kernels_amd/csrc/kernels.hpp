@@ -17,13 +17,15 @@ struct GemvPlan {
   int R = 1;        // 16-row tiles per wave (MFMA layout) or rows per wave (row-major layouts)
   int waves = 1;    // waves per workgroup, splitting K
   int MT = 1;       // 16-column activation tiles (MFMA GEMM)
-  int D = 4;        // chunk slots in flight per wave (M <= 8 GEMV)
+  int D = 4;        // chunk slots in flight per wave
+  int S = 1;        // workgroups splitting K per row group (MFMA GEMM)
 };
 
 // process-wide launch-shape override for tuning sweeps (lowbit_set_launch_override); 0 = automatic
 struct GemvOverride {
   int waves = 0;
   int ring = 0;
+  int splits = 0;
 };
 GemvOverride gemv_override();
 
@@ -34,6 +36,25 @@ constexpr int gemv_max_threads(int M, int R, int D = 4) {
 
 constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many bytes (the default dynamic LDS limit)
 
+// MFMA GEMM launch shape: K splits across workgroups up to kGemmMaxGroups workgroups (at most kMaxSplits ways), then
+// K-groups inside a workgroup up to kGemmTargetWaves waves. A workspace starts with kCounterBytes of arrival
+// counters (zero before first use, left zero by every launch), followed by the fp32 partial sums [splits][M][N].
+constexpr int kGemmMaxGroups = 320;
+constexpr int kGemmTargetWaves = 1792;
+constexpr int kMaxSplits = 32;
+constexpr size_t kCounterBytes = 16384;
+// (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
+// register budget of 4 KS waves per workgroup without spilling (hipcc -O3), and the LDS of the K-groups' x buffers
+constexpr bool gemm_fits(int MT, int RW, int D, int KS) {
+  if (KS == 4) return (MT == 1 && RW == 1 && D <= 3) || (MT == 1 && RW == 2 && D == 2) || (MT == 2 && RW == 1 && D == 2);
+  if (KS == 2)
+    return MT == 1 || (MT == 2 && (RW == 1 || D <= 3)) || (MT == 3 && (RW == 1 ? D <= 3 : D == 2)) ||
+           (MT == 4 && D == 2);
+  return !(MT == 4 && RW == 2 && D == 4);
+}
+constexpr int kMaxGroups = 2048;         // K / G limit of the MFMA-layout GEMV (scales staged in LDS)
+constexpr int64_t kMaxK = 1 << 22;       // K limit of the MFMA-layout kernels (32-bit buffer offsets)
+
 constexpr int kMaxClip = 64;
 struct ClipGrid {
   int n;                 // 0: plain absmax
@@ -41,12 +62,12 @@ struct ClipGrid {
 };
 
 GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave);
-GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles);
+GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes);
 int pick_rows_rowmajor(int N, int M);
 
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave);
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3);
-hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles);
+hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes);
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st);
 hipError_t relayout_launch(const uint8_t* src, uint8_t* dst, int N, int K, bool mfma, hipStream_t st);
 hipError_t quantize_launch(const void* w, int dtype, uint8_t* packed, f16* scales, int N, int K, int G,

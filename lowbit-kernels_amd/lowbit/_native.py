@@ -23,9 +23,9 @@ SIGNATURES = {
     "lowbit_last_error": ([], ctypes.c_char_p),
     "lowbit_strerror": ([_int], ctypes.c_char_p),
     "lowbit_version": ([], ctypes.c_char_p),
-    "lowbit_set_launch_override": ([_int, _int], _int),
+    "lowbit_set_launch_override": ([_int, _int, _int], _int),
     "lowbit_w4_gemv": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp], _int),
-    "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
+    "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
@@ -96,6 +96,23 @@ def _stream(device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+WORKSPACE_COUNTER_BYTES = 16384
+WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (16 << 20)     # LOWBIT_WORKSPACE_BYTES
+_WORKSPACES = {}
+
+
+def workspace(device, stream):
+    """The MFMA GEMM's workspace for (device, stream): zeroed once, kept for the life of the process (a graph captured
+    on the stream keeps using it), so calls on one stream never race on it and never reallocate it."""
+    import torch
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value)
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _check_tensors(x, w, s, group):
     """The tensor-metadata half of the reference's check() (csrc/w4_gemv.cu:312-325); sizes are checked natively."""
     import torch
@@ -140,8 +157,10 @@ class NativeExt:
         m, n = x.shape[0], w.shape[0]
         y = torch.empty((m, n), dtype=torch.float16, device=x.device)
         with _DeviceGuard(x.device):
+            st = _stream(x.device)
+            ws = workspace(x.device, st)
             check(self.lib.lowbit_w4_gemm_mfma(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group, int(row_tiles),
-                                               _stream(x.device)))
+                                               ptr(ws), ws.numel(), st))
         return y
 
     def w4_dequant(self, w, s, group, mma_layout=False):

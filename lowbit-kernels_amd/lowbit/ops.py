@@ -151,8 +151,11 @@ def dequant(wq, layout=None):
 
 # version 0 (auto) picks by batch size and layer width. The structure is the reference's (lowbit/ops.py:137-160):
 # the v6 GEMV up to AUTO_GEMV_ROWS rows; the MFMA kernel (v5) up to AUTO_V5_ROWS rows on every layer and up to
-# AUTO_V5_WIDE_ROWS rows on layers with N >= AUTO_WIDE_N; dequantize + BLAS beyond.
-AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 32, 64, 3072
+# AUTO_V5_WIDE_ROWS rows on layers with N >= AUTO_WIDE_N; dequantize + BLAS beyond. The constants come from an MI355X
+# sweep (graph-timed, weights cycled through >= 1 GiB, M in 1..64 on the Qwen2.5-3B/7B MLP shapes): the GEMV wins only
+# at M = 1; from M = 2 to 64 the MFMA kernel beats dequantize + hipBLASLt 2-6x and fp16 hipBLASLt on every shape, so
+# the width split of the reference's rule (which came from a T4) no longer matters.
+AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 64, 64, 3072
 
 
 def gemm_chunked(x, wq, chunk=64):

@@ -42,17 +42,22 @@ def _msg(rc):
     (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 96, 32, 6, 0, None), 7, "multiples of 128"),
     (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 3, None), 8, "rows_per_warp"),
     (lambda l: l.lowbit_w4_gemv(ctypes.c_void_p(4098), FAKE, FAKE, FAKE, 1, 16, 128, 128, 6, 0, None), 4, "16-byte"),
-    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 65, 16, 128, 128, 0, None), 5, "1..64 rows"),
-    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 3, None), 8, "row_tiles"),
-    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 192, 64, 0, None), 7, "multiples of 128"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 65, 16, 128, 128, 0, None, 0, None), 5, "1..64 rows"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 3, None, 0, None), 8, "row_tiles"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 192, 64, 0, None, 0, None), 7, "multiples of 128"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 0, ctypes.c_void_p(4104), 1 << 20, None),
+     1, "workspace"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 0, FAKE, 4096, None), 1, "workspace"),
+    (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 1 << 23, 128, 0, None, 0, None), 3, "K is at most"),
     (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 128, -1, 0, None), 2, "positive group size"),
     (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 96, 32, 1, None), 7, "group % 128"),
     (lambda l: l.lowbit_w4_quantize(FAKE, 0, FAKE, FAKE, 16, 128, 2048, None, 0, None), 2, "multiple of the group"),
     (lambda l: l.lowbit_w4_quantize(FAKE, 7, FAKE, FAKE, 16, 128, 128, None, 0, None), 1, "dtype"),
     (lambda l: l.lowbit_w4_relayout(FAKE, FAKE, 16, 128, 2, None), 1, "alias"),
     (lambda l: l.lowbit_w4_relayout(FAKE, ctypes.c_void_p(8192), 16, 96, 2, None), 7, "multiple of 128"),
-    (lambda l: l.lowbit_set_launch_override(3, 0), 8, "waves_per_group"),
-    (lambda l: l.lowbit_set_launch_override(4, 5), 8, "ring"),
+    (lambda l: l.lowbit_set_launch_override(3, 0, 0), 8, "waves_per_group"),
+    (lambda l: l.lowbit_set_launch_override(4, 5, 0), 8, "ring"),
+    (lambda l: l.lowbit_set_launch_override(4, 4, 33), 8, "k_splits"),
 ])
 def test_validation_refuses_before_any_gpu_call(call, code, text):
     rc = call(_native.lib())

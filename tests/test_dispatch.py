@@ -35,9 +35,10 @@ def test_auto_rule_on_the_mma_layout(calls, m, n, want):
     assert calls == [want]
 
 
-def test_reference_table_when_the_constants_are_the_t4_ones(calls):
-    if (ops.AUTO_GEMV_ROWS, ops.AUTO_V5_ROWS, ops.AUTO_V5_WIDE_ROWS, ops.AUTO_WIDE_N) != (1, 32, 64, 3072):
-        pytest.skip("the MI355X sweep moved the constants; _rule_cases covers their boundaries")
+def test_reference_table_with_the_t4_constants(calls, monkeypatch):
+    """The rule's structure reproduces the reference's own table when given the reference's (T4) constants."""
+    for name, value in (("AUTO_GEMV_ROWS", 1), ("AUTO_V5_ROWS", 32), ("AUTO_V5_WIDE_ROWS", 64), ("AUTO_WIDE_N", 3072)):
+        monkeypatch.setattr(ops, name, value)
     for m, n, want in [(1, 1024, 6), (2, 1024, 5), (32, 1024, 5), (33, 1024, "dequant"), (33, 4096, 5), (64, 4096, 5),
                        (65, 4096, "dequant")]:
         calls.clear()

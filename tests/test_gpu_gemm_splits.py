@@ -1,0 +1,99 @@
+"""The MFMA GEMM's launch shapes (row tiles per wave, ring slots, K split across workgroups with the workspace
+fixup) against the fp64 oracle, through the C ABI. Every shape must meet the same bound as the automatic one
+(max(4 x BLAS, 4 x fp16-output floor, 3e-3), bench/gpu_run.py:229-245), repeat bit for bit, and leave the
+workspace's arrival counters at zero; zero weights stay exactly zero under every split."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from lowbit import _native, ops
+from oracle import quant_ref as R
+
+from test_gpu_kernels import bound, make_weight, rel
+
+pytestmark = pytest.mark.gpu
+
+# (column tiles, row tiles per wave, ring slots, K-groups) the library builds: kernels.hpp gemm_fits
+def fits(mt, rw, d, ks):
+    if ks == 4:
+        return (mt, rw) == (1, 1) and d <= 3 or (mt, rw, d) in ((1, 2, 2), (2, 1, 2))
+    if ks == 2:
+        return mt == 1 or (mt == 2 and (rw == 1 or d <= 3)) or (mt == 3 and (d <= 3 if rw == 1 else d == 2)) or \
+            (mt == 4 and d == 2)
+    return (mt, rw, d) != (4, 2, 4)
+
+
+def gemm(x, wq, rw, d, splits, ws, ks=0):
+    lib = _native.lib()
+    n = wq.packed_mma.shape[0]
+    y = torch.empty(x.shape[0], n, dtype=torch.half, device="cuda")
+    _native.check(lib.lowbit_set_launch_override(4 * ks, d, splits))
+    try:
+        _native.check(lib.lowbit_w4_gemm_mfma(_native.ptr(x), _native.ptr(wq.packed_mma), _native.ptr(wq.scales),
+                                              _native.ptr(y), x.shape[0], n, x.shape[1], wq.group, rw,
+                                              _native.ptr(ws) if ws is not None else None,
+                                              ws.numel() if ws is not None else 0,
+                                              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    finally:
+        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+    return y
+
+
+@pytest.mark.parametrize("k,n", [(1024, 1001), (2048, 4096), (11008, 640), (384, 37), (3584, 200)])
+def test_every_launch_shape_against_fp64(cuda, k, n):
+    wq, ref_w, *_, gen = make_weight(k, n, k + 3 * n, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for m in (1, 3, 16, 17, 33, 64):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        ref = x.double() @ ref_w.T
+        lim = bound(x, ref_w, ref)
+        mt = (m + 15) // 16
+        for rw in (1, 2):
+            for d in (2, 3, 4):
+                for ks in (1, 2, 4):
+                    if not fits(mt, rw, d, ks):
+                        continue
+                    for splits in (1, 3, 32):
+                        y = gemm(x, wq, rw, d, splits, ws, ks)
+                        e = rel(y, ref)
+                        assert e <= lim, (k, n, m, rw, d, ks, splits, e, lim)
+                        assert torch.equal(y, gemm(x, wq, rw, d, splits, ws, ks)), (k, n, m, rw, d, ks, splits)
+        y0 = gemm(x, wq, 0, 0, 0, None)                  # no workspace: no split
+        assert rel(y0, ref) <= lim
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(ws[:_native.WORKSPACE_COUNTER_BYTES])) == 0
+
+
+def test_zero_weights_stay_zero_under_every_split(cuda):
+    rng = np.random.default_rng(5)
+    n, k = 96, 4096
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    w[::2] = 0.0
+    packed, scales = R.quantize_w4(w, 128)
+    wq = ops.W4Weight(packed, scales, 128, ("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for m in (2, 16, 40):
+        x = torch.from_numpy((rng.standard_normal((m, k)) * 30).astype(np.float16)).cuda()
+        ref = torch.from_numpy(R.gemv_reference(x.double().cpu().numpy(), packed, scales, 128)).cuda()
+        for splits, ks in ((1, 1), (2, 2), (7, 4), (16, 2)):
+            y = gemm(x, wq, 2, 2, splits, ws, ks)
+            assert torch.count_nonzero(y[:, ::2]) == 0, (m, splits)
+            assert rel(y, ref) <= R.REL_BOUND, (m, splits)
+
+
+def test_tiny_activations_keep_their_precision(cuda):
+    """Rows of tiny activations (down to fp16 subnormals) keep the same relative accuracy as rows of ordinary and of
+    large ones: every product is formed exactly, whatever the magnitude of x."""
+    wq, ref_w, *_, gen = make_weight(1024, 256, 99, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    x = torch.randn(4, 1024, generator=gen)
+    x[0] *= 1e-5
+    x[1] *= 3e-3
+    x[2, ::7] = 300.0
+    x = x.half().cuda()
+    ref = x.double() @ ref_w.T
+    for m in range(4):
+        ym = gemm(x, wq, 2, 4, 4, ws)[m:m + 1]
+        assert rel(ym, ref[m:m + 1]) <= R.REL_BOUND, m
