@@ -69,6 +69,8 @@ def parse():
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
     ap.add_argument("--sweep", choices=["skinny"], default=None)
+    ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
+                    help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--out", default=None)
     return ap.parse_args()
 
@@ -344,6 +346,118 @@ def pmc_workload(a):
                       "step_bytes": sum(alg_bytes(k, n) for _, k, n in projs)}), flush=True)
 
 
+# BASELINE configs 4 and 5: prompt length, greedy tokens, tokens per step of the teacher-forced feeds, clip search
+E2E = {"1.5b": dict(prompt=64, new=256, chunks=(1, 16, 48), feed=480, clip=False),
+       "3b": dict(prompt=512, new=256, chunks=(1, 16, 48), feed=480, clip=True),
+       "tiny": dict(prompt=32, new=32, chunks=(1, 16, 48), feed=96, clip=True)}
+
+
+def e2e(a):
+    """Random-init Qwen2.5 decoder, batch 1, every decode step one hipGraph (lowbit.decode.GraphDecoder): the fp16
+    model, then the same model with fake-quant weights (for agreement only) and with W4Linear (INT4 kernels).
+    Per model: TTFT (eager prefill of the prompt, dequantize + hipBLASLt for W4Linear), greedy decode tokens/s, and
+    tokens/s feeding a fixed random token stream 1, 16 and 48 tokens per step (GEMV, MFMA and MFMA kernels), plus
+    peak HBM. INT4 is compared with fake-quant on identical inputs (teacher-forced argmax agreement and max logit
+    difference relative to the logits' RMS, per tokens-per-step) and by the greedy sequences' common prefix."""
+    import torch
+    from lowbit import decode, model as lbmodel
+    cfg = E2E[a.e2e]
+    torch.cuda.set_device(0)
+    m = decode.random_model(a.e2e, seed=0)
+    vocab = m.config.vocab_size
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    prompt = torch.randint(0, vocab, (1, cfg["prompt"]), generator=gen, device="cuda")
+    feed = torch.randint(0, vocab, (cfg["feed"],), generator=gen, device="cuda")
+    max_len = cfg["prompt"] + max(cfg["new"], cfg["feed"]) + 64
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+
+    def measure(model, label, speed=True):
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        r = {"label": label}
+        dec = decode.GraphDecoder(model, max_len, chunk=1)
+        ttft = []
+        for _ in range(3 if speed else 1):
+            e0, e1 = ev(), ev()
+            e0.record()
+            first = dec.prefill(prompt).argmax(-1)
+            e1.record()
+            torch.cuda.synchronize()
+            ttft.append(e0.elapsed_time(e1))
+        dec.capture()
+        times, toks = [], None
+        for _ in range(3 if speed else 1):
+            first = dec.prefill(prompt).argmax(-1)
+            e0, e1 = ev(), ev()
+            e0.record()
+            toks = dec.greedy(first, cfg["new"])
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1))
+        ms = sorted(times)[len(times) // 2]
+        r["ttft_ms"] = round(sorted(ttft)[len(ttft) // 2], 3)
+        r["greedy"] = {"prompt_tokens": cfg["prompt"], "new_tokens": cfg["new"],
+                       "tokens_per_s": round((cfg["new"] - 1) / (ms / 1000), 1),
+                       "ms_per_token": round(ms / (cfg["new"] - 1), 4)}
+        logits = {}
+        for c in cfg["chunks"]:
+            dc = decode.GraphDecoder(model, max_len, chunk=c)
+            best, rows = None, []
+            for rep in range(2 if speed else 1):
+                dc.prefill(prompt)
+                if dc.graph is None:
+                    dc.capture()
+                rows = []
+                e0, e1 = ev(), ev()
+                e0.record()
+                for i in range(0, cfg["feed"], c):
+                    rows.append(dc.step(feed[i:i + c]).half().clone() if rep == 0 else dc.step(feed[i:i + c]))
+                e1.record()
+                torch.cuda.synchronize()
+                t = e0.elapsed_time(e1)
+                best = t if best is None else min(best, t)
+                if rep == 0:
+                    logits[c] = torch.cat(rows)
+            r[f"feed_{c}"] = {"tokens_per_step": c, "tokens": cfg["feed"],
+                              "tokens_per_s": round(cfg["feed"] / (best / 1000), 1)}
+            del dc
+        r["peak_hbm_bytes"] = torch.cuda.max_memory_allocated()
+        print(json.dumps({"e2e": a.e2e, **r}), flush=True)
+        return r, toks, logits
+
+    fp16, toks16, _ = measure(m, "fp16")
+    layers = lbmodel.quantize_layers(m, GROUP, CLIP_GRID if cfg["clip"] else None)
+    lbmodel.apply_fake_quant(layers)
+    fake, toks_fake, lg_fake = measure(m, "fake_quant", speed=False)
+    replaced, w4_bytes_total = lbmodel.apply_int4(layers)
+    int4, toks4, lg4 = measure(m, "int4_w4a16_g128" + ("_clip" if cfg["clip"] else ""))
+
+    def prefix(x, y):
+        diff = (x != y).nonzero()
+        return int(diff[0, 0]) if diff.numel() else int(x.numel())
+
+    agree = {}
+    for c in cfg["chunks"]:
+        f, q = lg_fake[c].float(), lg4[c].float()
+        rms = f.pow(2).mean().sqrt()
+        agree[str(c)] = {"argmax_agreement": round(float((f.argmax(-1) == q.argmax(-1)).float().mean()), 4),
+                         "max_logit_diff_rel": float((f - q).abs().max() / rms)}
+    res = {"e2e": a.e2e, "model": f"random-init Qwen2.5-{a.e2e} architecture (no checkpoint), fp16",
+           "layers_replaced": replaced, "int4_linear_bytes": w4_bytes_total, "clip_search": cfg["clip"],
+           "fp16": fp16, "fake_quant": fake, "int4": int4,
+           "int4_vs_fake_quant": agree,
+           "greedy_common_prefix": {"int4_vs_fake_quant": prefix(toks4, toks_fake), "int4_vs_fp16": prefix(toks4, toks16),
+                                    "of": cfg["new"]},
+           "speedup_greedy_graph": round(int4["greedy"]["tokens_per_s"] / fp16["greedy"]["tokens_per_s"], 3),
+           "speedup_feed": {str(c): round(int4[f"feed_{c}"]["tokens_per_s"] / fp16[f"feed_{c}"]["tokens_per_s"], 3)
+                            for c in cfg["chunks"]},
+           "ttft_ratio_int4_over_fp16": round(int4["ttft_ms"] / fp16["ttft_ms"], 3)}
+    print(json.dumps({k: v for k, v in res.items() if k not in ("fp16", "fake_quant", "int4")}), flush=True)
+    if a.out:
+        pathlib.Path(a.out).parent.mkdir(parents=True, exist_ok=True)
+        pathlib.Path(a.out).write_text(json.dumps(res, indent=1))
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -357,6 +471,8 @@ def main():
         pmc_workload(a)
     elif a.sweep == "skinny":
         sweep_skinny(a)
+    elif a.e2e:
+        e2e(a)
     else:
         contract(a)
 

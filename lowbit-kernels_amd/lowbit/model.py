@@ -1,62 +1,74 @@
-"""Swap a Hugging Face model's linear layers for INT4 weight-only ones (decode: gfx950 GEMV / MFMA kernels; prefill:
-dequantize + BLAS). Same surface as the reference's lowbit/model.py:1-57.
+"""INT4 weight-only projections for Hugging Face decoders: the reference's lowbit/model.py surface (W4Linear, TARGETS,
+quantize_layers, apply_fake_quant, apply_int4; lowbit/model.py:12-57) on the gfx950 library.
 
-Each layer is quantized once (quantize_layers); the same packed values then back either a "fake-quant" model
-(ordinary nn.Linear holding the dequantized fp16 weights, so PyTorch does the math) or the INT4 kernels. Equal quality
-from the two separates kernel error from quantization error.
+A model is quantized once (quantize_layers). The same packed values can then back a "fake-quant" model (its own
+nn.Linear layers holding the dequantized fp16 weights, so PyTorch does the arithmetic) or the INT4 kernels (W4Linear).
+Equal results from the two isolate kernel error from quantization error.
 """
 import torch
 from torch import nn
 
 from . import ops
 
+# the seven projections of a Qwen2 / Llama decoder layer; embeddings and the (tied) head stay fp16
 TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 
 class W4Linear(nn.Module):
-    """Drop-in for nn.Linear: reshape to [-1, in_features], fp16, ops.linear, then the bias (reference
-    lowbit/model.py:15-27)."""
+    """nn.Linear replacement holding an ops.W4Weight. forward flattens the leading dimensions, runs ops.linear in fp16
+    (GEMV / MFMA / dequantize + BLAS by row count, or a fixed `gemv_version`) and adds the bias in place."""
 
     def __init__(self, wq, bias, in_features, out_features, gemv_version=0):
         super().__init__()
-        self.in_features, self.out_features = in_features, out_features
-        self.wq, self.gemv_version = wq, gemv_version
-        self.bias = None if bias is None else nn.Parameter(bias.detach().half(), requires_grad=False)
+        self.wq = wq
+        self.in_features, self.out_features, self.gemv_version = in_features, out_features, gemv_version
+        if bias is None:
+            self.bias = None
+        else:
+            self.bias = nn.Parameter(bias.detach().to(torch.float16), requires_grad=False)
 
     def forward(self, x):
-        shape = x.shape
-        y = ops.linear(x.reshape(-1, self.in_features).half(), self.wq, version=self.gemv_version)
+        lead = x.shape[:-1]
+        y = ops.linear(x.reshape(-1, self.in_features).to(torch.float16), self.wq, version=self.gemv_version)
         if self.bias is not None:
-            y = y + self.bias
-        return y.reshape(*shape[:-1], self.out_features)
+            y.add_(self.bias)
+        return y.view(*lead, self.out_features)
+
+    def extra_repr(self):
+        return f"in_features={self.in_features}, out_features={self.out_features}, group={self.wq.group}"
+
+
+def _projections(model):
+    """(parent module, attribute name, nn.Linear) for every TARGETS projection, in module order."""
+    for parent in model.modules():
+        for name in TARGETS:
+            child = getattr(parent, name, None)
+            if isinstance(child, nn.Linear):
+                yield parent, name, child
 
 
 def quantize_layers(model, group=128, clip_grid=None):
-    """Quantize every decoder-layer projection once with the native GPU quantizer. Embeddings and lm_head stay fp16.
-    Returns [(parent, name, linear, packed, scales)] (reference lowbit/model.py:30-40)."""
-    out = []
-    for _, module in list(model.named_modules()):
-        for name, child in list(module.named_children()):
-            if isinstance(child, nn.Linear) and name in TARGETS:
-                packed, scales = ops.quantize_w4_gpu(child.weight, group, clip_grid)
-                out.append((module, name, child, packed, scales))
-    return out
+    """Quantize every projection with the GPU quantizer (absmax, or the clip search over `clip_grid`).
+    Returns a list of (parent, name, linear, packed, scales)."""
+    return [(parent, name, lin, *ops.quantize_w4_gpu(lin.weight, group, clip_grid))
+            for parent, name, lin in list(_projections(model))]
 
 
+@torch.no_grad()
 def apply_fake_quant(layers, group=128):
-    """Replace each weight by its dequantized fp16 value (exactly what the kernels multiply by)."""
+    """Overwrite each projection's weight with its dequantized fp16 value: exactly what the kernels multiply by."""
     for _, _, lin, packed, scales in layers:
-        lin.weight.data.copy_(ops.dequantize_w4_gpu(packed, scales, group))
+        lin.weight.copy_(ops.dequantize_w4_gpu(packed, scales, group))
 
 
 def apply_int4(layers, group=128, gemv_version=0, layouts=("mma",)):
-    """Swap each nn.Linear for a W4Linear on the same packed values; returns (layers replaced, INT4 bytes).
-    The device layouts are built on the GPU from the packed tensors (no host round trip)."""
-    count, nbytes = len(layers), 0
-    for parent, name, lin, packed, scales in layers:
+    """Swap every quantized projection for a W4Linear on the same packed values (device layouts built on the GPU).
+    Returns (layers replaced, INT4 bytes). Consumes `layers`, so the fp16 weights can be freed."""
+    replaced, nbytes = 0, 0
+    while layers:
+        parent, name, lin, packed, scales = layers.pop(0)
         wq = ops.W4Weight(packed, scales, group, layouts, device=packed.device)
         setattr(parent, name, W4Linear(wq, lin.bias, lin.in_features, lin.out_features, gemv_version))
-        nbytes += wq.nbytes()
-    layers.clear()                      # drops the last references to the fp16 nn.Linear weights
+        replaced, nbytes = replaced + 1, nbytes + wq.nbytes()
     torch.cuda.empty_cache()
-    return count, nbytes
+    return replaced, nbytes
