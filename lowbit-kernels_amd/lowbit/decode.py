@@ -75,24 +75,40 @@ class GraphDecoder:
     @torch.inference_mode()
     def prefill(self, ids):
         """Reset the cache and run the prompt ids [1, P] eagerly; returns the last position's logits."""
-        self.cache.reset()
         p = ids.shape[1]
+        if p > self.max_len:
+            raise ValueError(f"a {p}-token prompt does not fit a {self.max_len}-token cache")
+        self.cache.reset()
         out = self.m(input_ids=ids, past_key_values=self.cache,
                      cache_position=torch.arange(p, device=ids.device), use_cache=True)
         self.pos = p
         return out.logits[0, -1]
 
+    def _sync_write_position(self):
+        """Static cache layers (transformers >= 5) write new keys at a device-side counter of their own, advanced by
+        every forward, not at cache_position; put it at the decoder's position (so warm-up forwards cannot run it past
+        the end of the cache, and replays advance it in step with the decoder)."""
+        for layer in getattr(self.cache, "layers", ()):
+            n = getattr(layer, "cumulative_length", None)
+            if torch.is_tensor(n):
+                n.fill_(self.pos)
+
     @torch.inference_mode()
     def capture(self, warmup=3):
         """Warm up on a side stream (first calls allocate the cache layers and the library's workspaces), then
         capture one step. Must follow a prefill; the warm-up writes into cache rows past the prompt, which every
-        real step overwrites before reading."""
+        real step overwrites before reading. Each replay then advances the cache's write position and the decoder's
+        position together."""
+        if self.pos + self.chunk > self.max_len:
+            raise ValueError("the static cache has no room for a step after the prefill")
         self.positions.copy_(self.offsets + self.pos)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(warmup):
+                self._sync_write_position()          # every warm-up writes rows pos .. pos + chunk - 1 only
                 self._forward()
+            self._sync_write_position()
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
