@@ -103,6 +103,38 @@ int lowbit_w4_quantize(const void* w, int w_dtype, void* packed, void* scales, i
  * W4Weight (lowbit/ops.py:42-44, quant.interleave_for_gpu / interleave_for_mma). */
 int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int layout, void* stream);
 
+/* ---- decode-step fusions (no counterpart in the reference's extension; they replace the torch modules around the
+ * projections of a Qwen2 decoder layer, so that a graph-captured decode step issues ~9 launches per layer) ---- */
+
+#define LOWBIT_EPI_STORE 0     /* y = fp16(acc) */
+#define LOWBIT_EPI_BIAS 1      /* y = fp16(acc) + aux[n]                     (aux: bias [N]) */
+#define LOWBIT_EPI_RESIDUAL 2  /* y = aux[m][n] + fp16(acc)                  (aux: residual [M][N]; may equal y) */
+#define LOWBIT_EPI_SILU_MUL 3  /* rows interleaved 8 gate / 8 up per 16-row tile; y [M][N/2] = silu(gate) * up */
+
+/* A W4A16 projection on the MFMA layout with its consumer fused into the store: 1 <= M <= 64 (M = 1 runs the GEMV,
+ * otherwise the MFMA GEMM; workspace as for lowbit_w4_gemm_mfma). Each mode rounds as the unfused torch ops do
+ * (the projection to fp16 first; silu in fp32 then fp16, the product fp16), so results equal the unfused sequence
+ * (nn.Linear bias add of the reference's W4Linear, lowbit/model.py:25-26; the residual add and silu(gate) * up of
+ * transformers' Qwen2 layer). */
+int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* out[M][H] = weight * fp16(x / sqrt(mean(x^2) + eps)) (fp16 in/out, fp32 statistics; transformers Qwen2RMSNorm). */
+int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int64_t H, float eps, void* stream);
+
+/* RoPE (rotate-half, head_dim 128, angle = positions[m] * inv_freq[i] in fp32) on the q and k heads of a fused qkv
+ * projection output [M][(Hq + 2 Hkv) * 128]; rotated q -> q_out [M][Hq][128]; rotated k and v -> k_cache, v_cache
+ * [Hkv][L][128] at row positions[m] (device int64; rows outside 0..L-1 are not written). */
+int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
+                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, void* stream);
+
+/* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]
+ * (at most L); scores scaled by `scale`, softmax and P.V in fp32. max_keys: an upper bound on positions[m] + 1 over
+ * the calls that will run (sizes the launch; a captured graph keeps it). Hq / Hkv in {1, 2, 4, 6, 7, 8}. */
+int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
+                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* stream);
+
 /* ---- host-side format functions (CPU memory, no GPU needed); counterparts of lowbit/quant.py ---- */
 
 /* quant.quantize_w4 (lowbit/quant.py:23-35): w float32 [N, K] -> packed [N, K/2], scales fp16 bits [N, K/G]. */

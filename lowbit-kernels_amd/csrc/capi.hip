@@ -219,4 +219,66 @@ int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int lay
                     "w4_relayout");
 }
 
+int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
+  if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the fused projection takes 1..64 rows");
+  if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
+  if (int rc = check_mfma_layout_limits(N, K, group, M == 1)) return rc;
+  if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
+  if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
+    return fail(LOWBIT_ERR_ARG, "the bias and residual epilogues need aux");
+  if (epilogue == LOWBIT_EPI_SILU_MUL && (N % 16 || (reinterpret_cast<uintptr_t>(y) & 7)))
+    return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
+  if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
+    return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
+  a.epi.mode = epilogue;
+  a.epi.aux = static_cast<const f16*>(aux);
+  return hip_status(M == 1 ? gemv_mfma_layout_launch(a, 0) : gemm_mfma_launch(a, 0, workspace, workspace_bytes),
+                    "w4_linear_fused");
+}
+
+int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int64_t H, float eps, void* stream) {
+  if (!x || !weight || !out) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (M < 1 || H < 8 || H % 8 || !fits_int(M) || H > 65536) return fail(LOWBIT_ERR_SHAPE, "rmsnorm takes H % 8 == 0, H <= 65536");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out)) return fail(LOWBIT_ERR_ALIGN, "rmsnorm needs 16-byte aligned rows");
+  if (int rc = check_device()) return rc;
+  return hip_status(rmsnorm_launch(static_cast<const f16*>(x), static_cast<const f16*>(weight), static_cast<f16*>(out),
+                                   (int)M, (int)H, eps, static_cast<hipStream_t>(stream)),
+                    "rmsnorm");
+}
+
+int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
+                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, void* stream) {
+  if (!qkv || !positions || !inv_freq || !q_out || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (M < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || !fits_int(M * (Hq + 2 * Hkv) * 64) || !fits_int(L * 128 * Hkv))
+    return fail(LOWBIT_ERR_SHAPE, "rope_kv: M, Hq, Hkv (dividing Hq), L must be positive");
+  if (int rc = check_device()) return rc;
+  return hip_status(rope_kv_launch(static_cast<const f16*>(qkv), positions, inv_freq, static_cast<f16*>(q_out),
+                                   static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), (int)M, (int)Hq, (int)Hkv,
+                                   (int)L, static_cast<hipStream_t>(stream)),
+                    "rope_kv");
+}
+
+int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
+                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* stream) {
+  if (!q || !k_cache || !v_cache || !positions || !out) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (M < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || !fits_int(M * Hkv) || !fits_int(L * 128 * Hkv))
+    return fail(LOWBIT_ERR_SHAPE, "attention: M, Hq, Hkv (dividing Hq), L must be positive");
+  const int64_t g = Hq / Hkv;
+  if (!(g == 1 || g == 2 || g == 4 || g == 6 || g == 7 || g == 8))
+    return fail(LOWBIT_ERR_SHAPE, "attention takes 1, 2, 4, 6, 7 or 8 query heads per KV head");
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return fail(LOWBIT_ERR_ALIGN, "attention needs 16-byte aligned q and caches");
+  if (int rc = check_device()) return rc;
+  return hip_status(attention_launch(static_cast<const f16*>(q), static_cast<const f16*>(k_cache),
+                                     static_cast<const f16*>(v_cache), positions, static_cast<f16*>(out), (int)M,
+                                     (int)Hq, (int)Hkv, (int)L, (int)std::max<int64_t>(1, std::min(max_keys, L)), scale,
+                                     static_cast<hipStream_t>(stream)),
+                    "attention");
+}
+
 }  // extern "C"

@@ -115,6 +115,28 @@ __device__ __forceinline__ u32x4 load_stream(const void* p) {
 }
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// ---- output epilogues (the modes are listed with struct Epilogue in kernels.hpp) ----
+
+// y value for one output of the store / bias / residual modes
+__device__ __forceinline__ f16 epi_value(int mode, const f16* __restrict__ aux, float acc, int m, int n, int N) {
+  const f16 v = (f16)acc;
+  if (mode == 1) return v + aux[n];
+  if (mode == 2) return aux[(size_t)m * N + n] + v;
+  return v;
+}
+
+// silu(g) * u with the rounding of the torch ops it replaces: g and u rounded to fp16, silu evaluated in fp32 as
+// g / (1 + exp(-g)) and rounded, the product rounded
+__device__ __forceinline__ f16 silu_mul(float g, float u) {
+  const float g16 = (float)(f16)g;
+  const f16 s = (f16)(g16 / (1.0f + expf(-g16)));
+  return (f16)((float)s * (float)(f16)u);
+}
+
+__device__ __forceinline__ float shfl_down32(float v) {     // lane l gets lane l + 32 (lanes 32..63 get their own)
+  return __shfl_down(v, 32, 64);
+}
+
 // Launch on `stream` and report the launch status.
 template <typename... KArgs, typename... Args>
 inline hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t stream,

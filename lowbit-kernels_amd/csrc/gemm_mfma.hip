@@ -48,9 +48,9 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {   // value of lane 
 
 template <int MT, int RW, int D, int KS>
 __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
-                                                      const f16* __restrict__ s, f16* __restrict__ y, int M, int N,
-                                                      int K, int G, int S, uint32_t* __restrict__ ctr,
-                                                      float* __restrict__ part) {
+                                                      const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
+                                                      int S, uint32_t* __restrict__ ctr, float* __restrict__ part,
+                                                      Epilogue epi) {
   constexpr int T = kW * RW;                               // 16-row tiles per workgroup
   constexpr int kXBuf = 16 * MT * kXPitch;                 // one staged chunk of x
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -205,7 +205,26 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 
   // epilogue: K-group 0 holds the totals; the lane has rows n .. n + 3 of column m per (tile, column tile). Every
   // wave stays to the end, so each barrier below sees the whole workgroup.
-  const bool vec = (N & 3) == 0;
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+  // four outputs n .. n + 3 of column m (store / bias / residual), vectorized when aligned
+  auto store4 = [&](int m, int n, const f32x4& v) {
+    f16* dst = y + (size_t)m * N + n;
+    if (vec) {
+      const f16x2 lo = {epi_value(epi.mode, epi.aux, v[0], m, n, N), epi_value(epi.mode, epi.aux, v[1], m, n + 1, N)};
+      const f16x2 hi = {epi_value(epi.mode, epi.aux, v[2], m, n + 2, N), epi_value(epi.mode, epi.aux, v[3], m, n + 3, N)};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = epi_value(epi.mode, epi.aux, v[e], m, n + e, N);
+    }
+  };
+  // silu(gate rows n .. n + 3) * (up rows n + 8 .. n + 11) -> output columns 8 (n / 16) + n % 16 .. + 3
+  auto store4_silu = [&](int m, int n, const f32x4& g, const f32x4& u) {
+    f16* dst = y + (size_t)m * (N / 2) + 8 * (n >> 4) + (n & 15);
+    const f16x2 lo = {silu_mul(g[0], u[0]), silu_mul(g[1], u[1])}, hi = {silu_mul(g[2], u[2]), silu_mul(g[3], u[3])};
+    *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+  };
   if (S == 1) {
     if (kg > 0) return;
 #pragma unroll
@@ -213,17 +232,14 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
-        if (m >= M || n >= N) continue;
         const f32x4 v = acc[i][mt] * kTwo24;
-        f16* dst = y + (size_t)m * N + n;
-        if (vec) {
-          const f16x2 lo = {(f16)v[0], (f16)v[1]}, hi = {(f16)v[2], (f16)v[3]};
-          *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) dst[e] = (f16)v[e];
+        if (epi.mode == kEpiSiluMul) {                      // up rows 8 + 4 q + v sit 32 lanes on (q + 2)
+          const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
+          if (q < 2 && m < M && n < N) store4_silu(m, n, v, up);
+          continue;
         }
+        if (m >= M || n >= N) continue;
+        store4(m, n, v);
       }
     return;
   }
@@ -258,22 +274,24 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (tid == 0) __hip_atomic_store(ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nrows = min(16 * T, N - n0), nq = (nrows + 3) >> 2;
-  for (int it = tid; it < M * nq; it += 256 * KS) {
-    const int m = it / nq, n = n0 + 4 * (it - m * nq);
+  auto split_sum = [&](int m, int n) {                      // partials of rows n .. n + 3, added in split order
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    f16* dst = y + (size_t)m * N + n;
-    if (vec) {
+    if ((N & 3) == 0) {
       for (int sp = 0; sp < S; ++sp) sum += *reinterpret_cast<const f32x4*>(part + ((size_t)sp * M + m) * N + n);
-      const f16x2 lo = {(f16)sum[0], (f16)sum[1]}, hi = {(f16)sum[2], (f16)sum[3]};
-      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
     } else {
       for (int sp = 0; sp < S; ++sp)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (n + e < N) sum[e] += part[((size_t)sp * M + m) * N + n + e];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < N) dst[e] = (f16)sum[e];
+    }
+    return sum;
+  };
+  for (int it = tid; it < M * nq; it += 256 * KS) {
+    const int m = it / nq, n = n0 + 4 * (it - m * nq);
+    if (epi.mode == kEpiSiluMul) {
+      if ((n & 15) < 8) store4_silu(m, n, split_sum(m, n), split_sum(m, n + 8));
+    } else {
+      store4(m, n, split_sum(m, n));
     }
   }
 }
@@ -295,7 +313,7 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
       if (attr != hipSuccess) return attr;
     }
     return launch(kern, dim3(groups, p.S), dim3(256 * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G,
-                  p.S, ctr, part);
+                  p.S, ctr, part, a.epi);
   }
 }
 

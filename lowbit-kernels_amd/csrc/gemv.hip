@@ -53,7 +53,8 @@ template <int M, int R, int D, bool kLdsX>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
-                                                                           f16* __restrict__ y, int N, int K, int G) {
+                                                                           f16* y, int N, int K, int G,
+                                                                           Epilogue epi) {
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -228,7 +229,12 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       for (int m = 0; m < M; ++m) {
         const float v = quad_sum(acc[i][m]);
         const int n = 16 * (t0 + i) + r;
-        if (q == 0 && n < N) y[(size_t)m * N + n] = (f16)v;
+        if (epi.mode == kEpiSiluMul) {                      // row r + 8 (the up row) sits 32 lanes on
+          const float up = shfl_down32(v);
+          if (q == 0 && r < 8 && n < N) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
+        } else if (q == 0 && n < N) {
+          y[(size_t)m * N + n] = epi_value(epi.mode, epi.aux, v, m, n, N);
+        }
       }
     return;
   }
@@ -243,11 +249,21 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
   __syncthreads();
   for (int idx = threadIdx.x; idx < R * M * 16; idx += blockDim.x) {
-    float v = 0.f;
-    for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * 16) + idx];
     const int i = idx / (M * 16), m = (idx / 16) % M, rr = idx % 16;
     const int n = 16 * (t0 + i) + rr;
-    if (n < N) y[(size_t)m * N + n] = (f16)v;
+    if (epi.mode == kEpiSiluMul) {
+      if (rr >= 8 || n >= N) continue;
+      float g = 0.f, u = 0.f;
+      for (int wv2 = 0; wv2 < nwaves; ++wv2) {
+        g += red[wv2 * (R * M * 16) + idx];
+        u += red[wv2 * (R * M * 16) + idx + 8];
+      }
+      y[(size_t)m * (N / 2) + 8 * (t0 + i) + rr] = silu_mul(g, u);
+      continue;
+    }
+    float v = 0.f;
+    for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * 16) + idx];
+    if (n < N) y[(size_t)m * N + n] = epi_value(epi.mode, epi.aux, v, m, n, N);
   }
 }
 
@@ -312,9 +328,10 @@ hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const size_t x_bytes = (size_t)M * a.K * 2 + (size_t)M * (a.K / 32) * 8;
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
   if (x_bytes + s_bytes <= kGemvLdsX)
-    return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+    return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream,
+                  a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi);
   return launch(gemv_mfma_layout<M, R, D, false>, grid, block, std::max(s_bytes, red_bytes), a.stream,
-                a.x, a.w, a.s, a.y, a.N, a.K, a.G);
+                a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi);
 }
 
 template <int M>

@@ -4,6 +4,19 @@
 
 namespace lowbit {
 
+// What the MFMA-layout kernels do with each fp32 sum before storing it (all roundings as the unfused torch ops do
+// them: the product is rounded to fp16 first):
+//   kEpiStore     y[m][n] = fp16(acc)
+//   kEpiBias      y[m][n] = fp16(acc) + bias[n]                          (aux = bias [N])
+//   kEpiResidual  y[m][n] = residual[m][n] + fp16(acc)                   (aux = residual [M][N]; may be y itself)
+//   kEpiSiluMul   rows interleaved 8 gate, 8 up per 16-row tile; y [M][N/2] = silu(fp16(gate)) * fp16(up),
+//                 output column 8 t + r for gate row 16 t + r, up row 16 t + 8 + r
+enum : int { kEpiStore = 0, kEpiBias = 1, kEpiResidual = 2, kEpiSiluMul = 3 };
+struct Epilogue {
+  int mode = kEpiStore;
+  const f16* aux = nullptr;
+};
+
 struct GemvArgs {
   const f16* x;
   const uint8_t* w;
@@ -11,6 +24,7 @@ struct GemvArgs {
   f16* y;
   int M, N, K, G;
   hipStream_t stream;
+  Epilogue epi = {};
 };
 
 struct GemvPlan {
@@ -68,6 +82,11 @@ int pick_rows_rowmajor(int N, int M);
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave);
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3);
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes);
+hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st);
+hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
+                          f16* v_cache, int M, int Hq, int Hkv, int L, hipStream_t st);
+hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
+                            int Hkv, int L, int max_keys, float scale, hipStream_t st);
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st);
 hipError_t relayout_launch(const uint8_t* src, uint8_t* dst, int N, int K, bool mfma, hipStream_t st);
 hipError_t quantize_launch(const void* w, int dtype, uint8_t* packed, f16* scales, int N, int K, int G,

@@ -14,6 +14,7 @@ LIB_NAME = "liblowbit_w4.so"
 LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
 
 LAYOUT_CANONICAL, LAYOUT_V3, LAYOUT_MFMA, LAYOUT_NV_MMA = 0, 1, 2, 3
+EPI_STORE, EPI_BIAS, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2, 3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _LIB = None
@@ -29,6 +30,11 @@ SIGNATURES = {
     "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
+    "lowbit_w4_linear_fused": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp],
+                               _int),
+    "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
+    "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
+    "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp], _int),
     "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
     "lowbit_host_unpack": ([_vp, _vp, _i64, _i64], _int),
     "lowbit_host_dequantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
@@ -214,3 +220,44 @@ class NativeExt:
             check(self.lib.lowbit_w4_relayout(ptr(packed), ptr(out), packed.shape[0], packed.shape[1] * 2, int(layout),
                                               _stream(packed.device)))
         return out
+
+    # ---- decode-step fusions (lowbit_w4_linear_fused, lowbit_rmsnorm, lowbit_rope_kv, lowbit_attention) ----
+
+    def w4_linear_fused(self, x, w, s, group, epilogue, aux=None, out=None):
+        """x [M, K] (M <= 64) times the MFMA-layout weight with the epilogue fused into the store; returns y
+        ([M, N], or [M, N / 2] for EPI_SILU_MUL). `out` may be given (for EPI_RESIDUAL it may be `aux` itself)."""
+        import torch
+        _check_tensors(x, w, s, group)
+        m, n = x.shape[0], w.shape[0]
+        cols = n // 2 if epilogue == EPI_SILU_MUL else n
+        y = out if out is not None else torch.empty((m, cols), dtype=torch.float16, device=x.device)
+        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous():
+            raise RuntimeError("out must be a contiguous float16 [M, N] (or [M, N/2] for silu-mul) tensor")
+        if aux is not None and (aux.dtype != torch.float16 or not aux.is_contiguous() or aux.device != x.device):
+            raise RuntimeError("aux must be a contiguous float16 tensor on the same GPU")
+        with _DeviceGuard(x.device):
+            st = _stream(x.device)
+            ws = workspace(x.device, st)
+            check(self.lib.lowbit_w4_linear_fused(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group,
+                                                  int(epilogue), ptr(aux) if aux is not None else None, ptr(ws),
+                                                  ws.numel(), st))
+        return y
+
+    def rmsnorm(self, x, weight, eps, out=None):
+        import torch
+        y = out if out is not None else torch.empty_like(x)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_rmsnorm(ptr(x), ptr(weight), ptr(y), x.shape[0], x.shape[1], float(eps),
+                                          _stream(x.device)))
+        return y
+
+    def rope_kv(self, qkv, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv):
+        with _DeviceGuard(qkv.device):
+            check(self.lib.lowbit_rope_kv(ptr(qkv), ptr(positions), ptr(inv_freq), ptr(q_out), ptr(k_cache),
+                                          ptr(v_cache), qkv.shape[0], hq, hkv, k_cache.shape[1], _stream(qkv.device)))
+
+    def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale):
+        with _DeviceGuard(q.device):
+            check(self.lib.lowbit_attention(ptr(q), ptr(k_cache), ptr(v_cache), ptr(positions), ptr(out), q.shape[0],
+                                            hq, hkv, k_cache.shape[1], int(max_keys), float(scale),
+                                            _stream(q.device)))

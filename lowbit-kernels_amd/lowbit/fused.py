@@ -1,0 +1,208 @@
+"""A Qwen2 decoder forward assembled from the library's kernels, for batch-1 decoding with graph capture.
+
+The stock transformers modules issue about fifty launches per decoder layer and token on ROCm (RMSNorm as five
+elementwise ops, RoPE as six, bias and residual adds, cache index copies, mask construction); on MI355X, where a
+small launch costs ~3 us, that overhead, not the projections, dominates a decode step. FusedQwen2 runs one layer as
+
+    rmsnorm -> qkv projection (+bias) -> rope + cache write -> attention -> o projection (+residual, in place)
+    -> rmsnorm -> gate|up projection (silu(gate) * up) -> down projection (+residual, in place)
+
+with its own KV cache. The projections are either W4A16 (lowbit_w4_linear_fused: GEMV / MFMA kernels with the
+consumer fused into the store, for up to 64 rows; dequantize + hipBLASLt beyond) or fp16 (hipBLASLt through torch,
+bias and residual folded into addmm, silu * up as two torch ops), so the two variants share every other kernel and
+differ only in the projections. Weights come from a transformers Qwen2ForCausalLM; q|k|v are merged into one
+projection and gate|up into another, their rows interleaved 8 gate / 8 up per 16-row tile for the silu epilogue.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+from . import _native, ops
+
+EPI_STORE, EPI_BIAS, EPI_RESIDUAL, EPI_SILU_MUL = (_native.EPI_STORE, _native.EPI_BIAS, _native.EPI_RESIDUAL,
+                                                   _native.EPI_SILU_MUL)
+
+
+def interleave_gate_up(gate, up):
+    """Rows [g0..g7, u0..u7, g8..g15, u8..u15, ...] of two [I, ...] tensors (I % 8 == 0)."""
+    i = gate.shape[0]
+    if i % 8 or up.shape[0] != i:
+        raise ValueError("gate and up need the same row count, a multiple of 8")
+    rest = gate.shape[1:]
+    return torch.stack([gate.reshape(i // 8, 8, *rest), up.reshape(i // 8, 8, *rest)], 1).reshape(2 * i, *rest)
+
+
+class _W4:
+    """A merged W4A16 projection: W4Weight on the MFMA layout plus its bias."""
+
+    def __init__(self, packed, scales, group, bias=None):
+        self.wq = ops.W4Weight(packed, scales, group, ("mma",), device=packed.device)
+        self.bias = bias
+
+    def __call__(self, x, epilogue, aux=None, out=None):
+        wq = self.wq
+        if x.shape[0] <= 64:
+            return ops.ext().w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out)
+        w = ops.dequant(wq)                                  # prefill: dequantize + hipBLASLt, epilogue in torch
+        return _torch_epilogue(x, w, epilogue, aux, out)
+
+
+class _F16:
+    """A merged fp16 projection (hipBLASLt through torch)."""
+
+    def __init__(self, weight, bias=None):
+        self.w, self.bias = weight, bias
+
+    def __call__(self, x, epilogue, aux=None, out=None):
+        return _torch_epilogue(x, self.w, epilogue, aux, out)
+
+
+def _torch_epilogue(x, w, epilogue, aux, out):
+    if epilogue == EPI_BIAS:
+        return torch.addmm(aux, x, w.t(), out=out) if out is not None else torch.addmm(aux, x, w.t())
+    if epilogue == EPI_RESIDUAL:
+        if out is not None and out.data_ptr() == aux.data_ptr():
+            return out.addmm_(x, w.t())
+        return torch.addmm(aux, x, w.t(), out=out) if out is not None else torch.addmm(aux, x, w.t())
+    y = F.linear(x, w)
+    if epilogue == EPI_SILU_MUL:
+        m = y.shape[0]
+        gu = y.view(m, -1, 2, 8)
+        r = (F.silu(gu[:, :, 0]) * gu[:, :, 1]).reshape(m, -1)
+        return out.copy_(r) if out is not None else r
+    return out.copy_(y) if out is not None else y
+
+
+class FusedQwen2:
+    """Batch-1 Qwen2 forward from the library's kernels (see the module docstring).
+
+    build(model, max_len, quant, group, clip_grid): quant = "int4" quantizes every projection with the GPU quantizer
+    (the same bits as lowbit.model.quantize_layers) and keeps only the packed weights; quant = "fp16" keeps fp16
+    copies of the merged weights. forward(tokens [M], positions [M]) -> logits [M, vocab]; the KV cache rows at
+    `positions` are written, rows 0..position are attended.
+    """
+
+    def __init__(self, model, max_len, quant="int4", group=128, clip_grid=None):
+        cfg = model.config
+        self.hidden, self.hq, self.hkv = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads
+        self.head_dim = getattr(cfg, "head_dim", None) or self.hidden // self.hq
+        if self.head_dim != 128:
+            raise ValueError("the fused attention kernels take head_dim 128")
+        self.eps, self.max_len, self.quant = cfg.rms_norm_eps, max_len, quant
+        dev = model.model.embed_tokens.weight.device
+        self.embed = model.model.embed_tokens.weight.detach()
+        self.head = model.lm_head.weight.detach()
+        self.final_norm = model.model.norm.weight.detach()
+        self.inv_freq = model.model.rotary_emb.inv_freq.detach().float().contiguous()
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+        self.layers = []
+        for layer in model.model.layers:
+            att, mlp = layer.self_attn, layer.mlp
+            qkv_w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).detach()
+            qkv_b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).detach().half().contiguous()
+            gu_w = interleave_gate_up(mlp.gate_proj.weight.detach(), mlp.up_proj.weight.detach())
+            ws = {"qkv": qkv_w, "o": att.o_proj.weight.detach(), "gu": gu_w, "down": mlp.down_proj.weight.detach()}
+            if quant == "int4":
+                proj = {}
+                for name, w in ws.items():
+                    packed, scales = ops.quantize_w4_gpu(w, group, clip_grid)
+                    proj[name] = _W4(packed, scales, group)
+            elif quant == "fp16":
+                proj = {name: _F16(w.half().contiguous()) for name, w in ws.items()}
+            else:
+                raise ValueError("quant is 'int4' or 'fp16'")
+            proj["qkv"].bias = qkv_b
+            self.layers.append({"in_norm": layer.input_layernorm.weight.detach(),
+                                "post_norm": layer.post_attention_layernorm.weight.detach(), **proj})
+        n = len(self.layers)
+        self.k_cache = torch.zeros(n, self.hkv, max_len, self.head_dim, dtype=torch.float16, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+
+    def reset(self):
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+    @torch.inference_mode()
+    def forward(self, tokens, positions):
+        """tokens, positions: int64 [M] on the GPU -> logits fp16 [M, vocab]."""
+        ext = ops.ext()
+        m = tokens.shape[0]
+        h = F.embedding(tokens, self.embed)
+        xn = torch.empty_like(h)
+        q = torch.empty(m, self.hq, self.head_dim, dtype=torch.float16, device=h.device)
+        attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
+        for i, lay in enumerate(self.layers):
+            ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
+            qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
+            ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
+            ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
+                          self.scale)
+            lay["o"](attn, EPI_RESIDUAL, h, out=h)
+            ext.rmsnorm(h, lay["post_norm"], self.eps, out=xn)
+            act = lay["gu"](xn, EPI_SILU_MUL)
+            lay["down"](act, EPI_RESIDUAL, h, out=h)
+        ext.rmsnorm(h, self.final_norm, self.eps, out=xn)
+        return F.linear(xn, self.head)
+
+    __call__ = forward
+
+
+class FusedDecoder:
+    """GraphDecoder's interface (prefill / capture / step / greedy) over a FusedQwen2."""
+
+    def __init__(self, fused, chunk=1):
+        self.f, self.chunk = fused, chunk
+        dev = fused.embed.device
+        self.tokens = torch.zeros(chunk, dtype=torch.long, device=dev)
+        self.positions = torch.zeros(chunk, dtype=torch.long, device=dev)
+        self.offsets = torch.arange(chunk, dtype=torch.long, device=dev)
+        self.pos = 0
+        self.graph = self.logits = self.next_token = None
+
+    @torch.inference_mode()
+    def prefill(self, ids):
+        p = ids.shape[-1]
+        if p > self.f.max_len:
+            raise ValueError(f"a {p}-token prompt does not fit a {self.f.max_len}-token cache")
+        self.f.reset()
+        logits = self.f(ids.view(-1), torch.arange(p, device=ids.device))
+        self.pos = p
+        return logits[-1]
+
+    @torch.inference_mode()
+    def capture(self, warmup=2):
+        if self.pos + self.chunk > self.f.max_len:
+            raise ValueError("the cache has no room for a step after the prefill")
+        self.positions.copy_(self.offsets + self.pos)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.f(self.tokens, self.positions)
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self.f(self.tokens, self.positions)
+            self.next_token = self.logits[-1].argmax(-1)
+        return self
+
+    def step(self, tokens):
+        if self.pos + self.chunk > self.f.max_len:
+            raise ValueError("the cache is full")
+        self.tokens.copy_(tokens.view(self.chunk))
+        self.positions.copy_(self.offsets + self.pos)
+        self.graph.replay()
+        self.pos += self.chunk
+        return self.logits
+
+    @torch.inference_mode()
+    def greedy(self, first, n):
+        if self.chunk != 1:
+            raise ValueError("greedy decoding feeds one token per step")
+        out = torch.empty(n, dtype=torch.long, device=self.tokens.device)
+        out[0] = first
+        for i in range(1, n):
+            self.step(out[i - 1])
+            out[i] = self.next_token
+        return out

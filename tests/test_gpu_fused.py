@@ -1,0 +1,141 @@
+"""The decode-step fusions on the GPU, through the C ABI:
+* lowbit_w4_linear_fused: the bias and residual epilogues give exactly the unfused result (the same kernel's sum,
+  then the torch add); silu-mul equals torch's silu(gate) * up on the unfused outputs; GEMV (M = 1) and MFMA paths,
+  with and without the split of K;
+* lowbit_rmsnorm and lowbit_rope_kv against transformers' own Qwen2RMSNorm and apply_rotary_pos_emb;
+* lowbit_attention against an fp32 causal softmax attention;
+* FusedQwen2 (fp16 and int4) against the transformers model on the same tokens."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from lowbit import _native, decode, fused, model as lbmodel, ops
+
+from test_gpu_kernels import make_weight, rel
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp_diff(a, b):
+    return int((a.view(torch.int16).int() - b.view(torch.int16).int()).abs().max())
+
+
+@pytest.mark.parametrize("k,n", [(1024, 512), (2048, 2560), (11008, 2048), (384, 4096)])
+def test_epilogues_equal_the_unfused_ops(cuda, k, n):
+    wq, _, *_, gen = make_weight(k, n, k + n, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    for m in (1, 3, 16, 40):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        plain = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_STORE)
+        unfused = ops.gemv(x, wq, 6 if m == 1 else 5)
+        assert torch.equal(plain, unfused), m
+        assert torch.equal(ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias),
+                           plain + bias), m
+        res = torch.randn(m, n, generator=gen).half().cuda()
+        want = res + plain
+        got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_RESIDUAL, res)
+        assert torch.equal(got, want), m
+        ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_RESIDUAL, res, out=res)   # in place
+        assert torch.equal(res, want), m
+        gu = plain.view(m, -1, 2, 8)
+        want = (F.silu(gu[:, :, 0]) * gu[:, :, 1]).reshape(m, -1)
+        got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL)
+        assert ulp_diff(got, want) <= 1 and float((got != want).float().mean()) < 0.01, m
+
+
+def test_rmsnorm_matches_qwen2_rmsnorm(cuda):
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
+    g = torch.Generator().manual_seed(1)
+    for h in (256, 1536, 2048, 3584):
+        norm = Qwen2RMSNorm(h, eps=1e-6).cuda().half()
+        with torch.no_grad():
+            norm.weight.copy_((1 + 0.1 * torch.randn(h, generator=g)).half())
+        x = (torch.randn(5, h, generator=g) * 3).half().cuda()
+        want = norm(x)
+        got = ops.ext().rmsnorm(x, norm.weight.detach(), 1e-6)
+        assert ulp_diff(got, want) <= 1, h
+
+
+def test_rope_and_cache_write_match_transformers(cuda):
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    m = decode.random_model("tiny", seed=2)
+    hq, hkv, L = 2, 1, 64
+    g = torch.Generator(device="cuda").manual_seed(3)
+    pos = torch.tensor([0, 5, 17, 63], device="cuda")
+    qkv = torch.randn(4, (hq + 2 * hkv) * 128, generator=g, device="cuda").half()
+    q_out = torch.empty(4, hq, 128, dtype=torch.half, device="cuda")
+    k_cache = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+    v_cache = torch.zeros_like(k_cache)
+    ops.ext().rope_kv(qkv, pos, m.model.rotary_emb.inv_freq.float(), q_out, k_cache, v_cache, hq, hkv)
+    cos, sin = m.model.rotary_emb(qkv.view(1, 4, -1), pos.view(1, -1))
+    q = qkv[:, :hq * 128].view(1, 4, hq, 128).transpose(1, 2)
+    k = qkv[:, hq * 128:(hq + hkv) * 128].view(1, 4, hkv, 128).transpose(1, 2)
+    q_ref, k_ref = apply_rotary_pos_emb(q, k, cos, sin)
+    assert ulp_diff(q_out, q_ref[0].transpose(0, 1).contiguous()) <= 1
+    assert ulp_diff(k_cache[:, pos], k_ref[0]) <= 1
+    assert torch.equal(v_cache[:, pos], qkv[:, (hq + hkv) * 128:].view(4, hkv, 128).transpose(0, 1))
+    rest = torch.ones(L, dtype=torch.bool, device="cuda")
+    rest[pos] = False
+    assert int(torch.count_nonzero(k_cache[:, rest])) == 0 and int(torch.count_nonzero(v_cache[:, rest])) == 0
+
+
+@pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
+                                                (28, 4, 300, list(range(200, 248))), (2, 1, 64, [10, 40])])
+def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
+    g = torch.Generator(device="cuda").manual_seed(hq + L)
+    m = len(positions)
+    q = torch.randn(m, hq, 128, generator=g, device="cuda").half()
+    k_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
+    v_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
+    pos = torch.tensor(positions, device="cuda")
+    out = torch.empty(m, hq * 128, dtype=torch.half, device="cuda")
+    scale = 1 / math.sqrt(128)
+    ops.ext().attention(q, k_cache, v_cache, pos, out, hq, hkv, L, scale)
+    grp = hq // hkv
+    ref = torch.empty(m, hq, 128, dtype=torch.float32, device="cuda")
+    for i, p in enumerate(positions):
+        for h in range(hq):
+            kk, vv = k_cache[h // grp, :p + 1].float(), v_cache[h // grp, :p + 1].float()
+            w = torch.softmax(kk @ q[i, h].float() * scale, 0)
+            ref[i, h] = w @ vv
+    assert rel(out.view(m, hq, 128), ref.double()) < 3e-3
+
+
+@pytest.fixture(scope="module")
+def tiny_models():
+    torch.cuda.set_device(0)
+    return decode.random_model("tiny", seed=21)
+
+
+def test_fused_qwen2_matches_transformers(cuda, tiny_models):
+    m = tiny_models
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    prompt = torch.randint(0, 1024, (1, 70), generator=gen, device="cuda")
+    feed = torch.randint(0, 1024, (16,), generator=gen, device="cuda")
+    with torch.inference_mode():
+        ref = m(torch.cat([prompt[0], feed]).view(1, -1)).logits[0, 70:].float()
+    f16 = fused.FusedQwen2(m, 128, quant="fp16")
+    dec = fused.FusedDecoder(f16, chunk=1)
+    dec.prefill(prompt)
+    dec.capture()
+    rows = [dec.step(feed[i:i + 1]).float().clone() for i in range(16)]
+    got = torch.cat(rows)
+    # step i feeds feed[i] at position 70 + i: its logits are the full-sequence forward's at that position
+    err = float((got - ref).abs().max() / ref.pow(2).mean().sqrt())
+    assert err < 2e-2, err
+    assert float((got.argmax(-1) == ref.argmax(-1)).float().mean()) >= 0.9
+    # int4: same quantized weights as lowbit.model's W4Linear path (fake-quant reference in torch)
+    q4 = fused.FusedQwen2(m, 128, quant="int4")
+    d4 = fused.FusedDecoder(q4, chunk=16)
+    d4.prefill(prompt)
+    d4.capture()
+    got4 = d4.step(feed).float()
+    layers = lbmodel.quantize_layers(m, 128)
+    lbmodel.apply_fake_quant(layers)
+    with torch.inference_mode():
+        ref4 = m(torch.cat([prompt[0], feed]).view(1, -1)).logits[0, 70:].float()
+    err4 = float((got4 - ref4).abs().max() / ref4.pow(2).mean().sqrt())
+    assert err4 < 2e-2, err4
