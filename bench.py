@@ -353,14 +353,17 @@ E2E = {"1.5b": dict(prompt=64, new=256, chunks=(1, 16, 48), feed=480, clip=False
 
 
 def e2e(a):
-    """Random-init Qwen2.5 decoder, batch 1, every decode step one hipGraph (lowbit.decode.GraphDecoder): the fp16
-    model, then the same model with fake-quant weights (for agreement only) and with W4Linear (INT4 kernels).
-    Per model: TTFT (eager prefill of the prompt, dequantize + hipBLASLt for W4Linear), greedy decode tokens/s, and
-    tokens/s feeding a fixed random token stream 1, 16 and 48 tokens per step (GEMV, MFMA and MFMA kernels), plus
-    peak HBM. INT4 is compared with fake-quant on identical inputs (teacher-forced argmax agreement and max logit
-    difference relative to the logits' RMS, per tokens-per-step) and by the greedy sequences' common prefix."""
+    """Random-init Qwen2.5 decoder, batch 1, every decode step one hipGraph. Two pairs of variants:
+    * transformers' own modules (lowbit.decode.GraphDecoder): fp16, then the same model with W4Linear projections
+      (the reference's drop-in, lowbit/model.py), plus fake-quant (dequantized weights in nn.Linear) for agreement;
+    * FusedQwen2 (lowbit.fused: RMSNorm, RoPE + cache write and attention kernels, merged q|k|v and gate|up with fused
+      epilogues), fp16 projections (hipBLASLt) vs W4A16 projections; everything but the projections is shared.
+    Per variant: TTFT (eager prefill of the prompt: dequantize + hipBLASLt for W4), greedy decode tokens/s, tokens/s
+    feeding a fixed random stream 1, 16 and 48 tokens per step (GEMV / MFMA / MFMA kernels), peak HBM. W4 variants
+    are compared with fake-quant on identical inputs (teacher-forced argmax agreement, max logit difference relative
+    to the logits' RMS)."""
     import torch
-    from lowbit import decode, model as lbmodel
+    from lowbit import decode, fused, model as lbmodel
     cfg = E2E[a.e2e]
     torch.cuda.set_device(0)
     m = decode.random_model(a.e2e, seed=0)
@@ -369,18 +372,20 @@ def e2e(a):
     prompt = torch.randint(0, vocab, (1, cfg["prompt"]), generator=gen, device="cuda")
     feed = torch.randint(0, vocab, (cfg["feed"],), generator=gen, device="cuda")
     max_len = cfg["prompt"] + max(cfg["new"], cfg["feed"]) + 64
+    clip = CLIP_GRID if cfg["clip"] else None
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
 
-    def measure(model, label, speed=True):
+    def measure(make, label, speed=True):
+        """make(chunk) -> a decoder (prefill / capture / step / greedy)."""
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
         r = {"label": label}
-        dec = decode.GraphDecoder(model, max_len, chunk=1)
+        dec = make(1)
         ttft = []
         for _ in range(3 if speed else 1):
             e0, e1 = ev(), ev()
             e0.record()
-            first = dec.prefill(prompt).argmax(-1)
+            dec.prefill(prompt).argmax(-1)
             e1.record()
             torch.cuda.synchronize()
             ttft.append(e0.elapsed_time(e1))
@@ -399,10 +404,11 @@ def e2e(a):
         r["greedy"] = {"prompt_tokens": cfg["prompt"], "new_tokens": cfg["new"],
                        "tokens_per_s": round((cfg["new"] - 1) / (ms / 1000), 1),
                        "ms_per_token": round(ms / (cfg["new"] - 1), 4)}
+        del dec
         logits = {}
         for c in cfg["chunks"]:
-            dc = decode.GraphDecoder(model, max_len, chunk=c)
-            best, rows = None, []
+            dc = make(c)
+            best = None
             for rep in range(2 if speed else 1):
                 dc.prefill(prompt)
                 if dc.graph is None:
@@ -411,7 +417,9 @@ def e2e(a):
                 e0, e1 = ev(), ev()
                 e0.record()
                 for i in range(0, cfg["feed"], c):
-                    rows.append(dc.step(feed[i:i + c]).half().clone() if rep == 0 else dc.step(feed[i:i + c]))
+                    out = dc.step(feed[i:i + c])
+                    if rep == 0:
+                        rows.append(out.half().clone())
                 e1.record()
                 torch.cuda.synchronize()
                 t = e0.elapsed_time(e1)
@@ -425,34 +433,52 @@ def e2e(a):
         print(json.dumps({"e2e": a.e2e, **r}), flush=True)
         return r, toks, logits
 
-    fp16, toks16, _ = measure(m, "fp16")
-    layers = lbmodel.quantize_layers(m, GROUP, CLIP_GRID if cfg["clip"] else None)
+    hf_dec = lambda model: (lambda c: decode.GraphDecoder(model, max_len, c))  # noqa: E731
+    res = {"e2e": a.e2e, "model": f"random-init Qwen2.5-{a.e2e} architecture (no checkpoint), fp16",
+           "clip_search": cfg["clip"], "workload": cfg}
+    out, tok, lg = {}, {}, {}
+    out["hf_fp16"], tok["hf_fp16"], lg["hf_fp16"] = measure(hf_dec(m), "hf_fp16")
+    fq = fused.FusedQwen2(m, max_len, quant="fp16")
+    out["fused_fp16"], tok["fused_fp16"], lg["fused_fp16"] = measure(lambda c: fused.FusedDecoder(fq, c), "fused_fp16")
+    del fq
+    fq = fused.FusedQwen2(m, max_len, quant="int4", clip_grid=clip)
+    out["fused_int4"], tok["fused_int4"], lg["fused_int4"] = measure(lambda c: fused.FusedDecoder(fq, c), "fused_int4")
+    del fq
+    torch.cuda.empty_cache()
+    layers = lbmodel.quantize_layers(m, GROUP, clip)
     lbmodel.apply_fake_quant(layers)
-    fake, toks_fake, lg_fake = measure(m, "fake_quant", speed=False)
-    replaced, w4_bytes_total = lbmodel.apply_int4(layers)
-    int4, toks4, lg4 = measure(m, "int4_w4a16_g128" + ("_clip" if cfg["clip"] else ""))
+    out["hf_fake_quant"], tok["hf_fake_quant"], lg["hf_fake_quant"] = measure(hf_dec(m), "hf_fake_quant", speed=False)
+    res["layers_replaced"], res["int4_linear_bytes"] = lbmodel.apply_int4(layers)
+    out["hf_int4"], tok["hf_int4"], lg["hf_int4"] = measure(hf_dec(m), "hf_int4")
 
     def prefix(x, y):
         diff = (x != y).nonzero()
         return int(diff[0, 0]) if diff.numel() else int(x.numel())
 
-    agree = {}
-    for c in cfg["chunks"]:
-        f, q = lg_fake[c].float(), lg4[c].float()
-        rms = f.pow(2).mean().sqrt()
-        agree[str(c)] = {"argmax_agreement": round(float((f.argmax(-1) == q.argmax(-1)).float().mean()), 4),
-                         "max_logit_diff_rel": float((f - q).abs().max() / rms)}
-    res = {"e2e": a.e2e, "model": f"random-init Qwen2.5-{a.e2e} architecture (no checkpoint), fp16",
-           "layers_replaced": replaced, "int4_linear_bytes": w4_bytes_total, "clip_search": cfg["clip"],
-           "fp16": fp16, "fake_quant": fake, "int4": int4,
-           "int4_vs_fake_quant": agree,
-           "greedy_common_prefix": {"int4_vs_fake_quant": prefix(toks4, toks_fake), "int4_vs_fp16": prefix(toks4, toks16),
-                                    "of": cfg["new"]},
-           "speedup_greedy_graph": round(int4["greedy"]["tokens_per_s"] / fp16["greedy"]["tokens_per_s"], 3),
-           "speedup_feed": {str(c): round(int4[f"feed_{c}"]["tokens_per_s"] / fp16[f"feed_{c}"]["tokens_per_s"], 3)
-                            for c in cfg["chunks"]},
-           "ttft_ratio_int4_over_fp16": round(int4["ttft_ms"] / fp16["ttft_ms"], 3)}
-    print(json.dumps({k: v for k, v in res.items() if k not in ("fp16", "fake_quant", "int4")}), flush=True)
+    def agree(x, y):
+        r = {}
+        for c in cfg["chunks"]:
+            f, q = lg[y][c].float(), lg[x][c].float()
+            rms = f.pow(2).mean().sqrt()
+            r[str(c)] = {"argmax_agreement": round(float((f.argmax(-1) == q.argmax(-1)).float().mean()), 4),
+                         "max_logit_diff_rel": round(float((f - q).abs().max() / rms), 5)}
+        return r
+
+    res["agreement"] = {"hf_int4_vs_hf_fake_quant": agree("hf_int4", "hf_fake_quant"),
+                        "fused_int4_vs_hf_fake_quant": agree("fused_int4", "hf_fake_quant"),
+                        "fused_fp16_vs_hf_fp16": agree("fused_fp16", "hf_fp16")}
+    res["greedy_common_prefix"] = {"hf_int4_vs_hf_fake_quant": prefix(tok["hf_int4"], tok["hf_fake_quant"]),
+                                   "fused_int4_vs_hf_fake_quant": prefix(tok["fused_int4"], tok["hf_fake_quant"]),
+                                   "fused_fp16_vs_hf_fp16": prefix(tok["fused_fp16"], tok["hf_fp16"]),
+                                   "of": cfg["new"]}
+    sp = lambda x, y, k: round(out[x][k]["tokens_per_s"] / out[y][k]["tokens_per_s"], 3)  # noqa: E731
+    keys = ["greedy"] + [f"feed_{c}" for c in cfg["chunks"]]
+    res["speedup_w4_over_fp16"] = {"transformers_modules": {k: sp("hf_int4", "hf_fp16", k) for k in keys},
+                                   "fused_layer": {k: sp("fused_int4", "fused_fp16", k) for k in keys},
+                                   "fused_w4_over_transformers_fp16": {k: sp("fused_int4", "hf_fp16", k) for k in keys}}
+    res["ttft_ms"] = {k: v["ttft_ms"] for k, v in out.items()}
+    res["variants"] = out
+    print(json.dumps({k: v for k, v in res.items() if k != "variants"}), flush=True)
     if a.out:
         pathlib.Path(a.out).parent.mkdir(parents=True, exist_ok=True)
         pathlib.Path(a.out).write_text(json.dumps(res, indent=1))
