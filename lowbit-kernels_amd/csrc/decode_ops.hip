@@ -88,95 +88,101 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
 }
 
 // Causal GQA attention for M query tokens at positions pos[m] over the cache rows 0 .. pos[m]:
-// out[m][h * D + d] = sum_j softmax_j(scale * q[m][h] . k[j]) v[j][d], for the G = Hq / Hkv query heads of KV head hk.
-// One block of W waves per (token, KV head). Each wave takes blocks of 64 keys (key w * 64 + 64 W b + lane):
-// scores with the lane holding one key, an online softmax per head in fp32, then P V with the lane holding two of
-// the 128 output dims. The waves' partial states are merged through LDS at the end.
-template <int G>
-__global__ __launch_bounds__(1024) void attention_kernel(const f16* __restrict__ q, const f16* __restrict__ k_cache,
-                                                         const f16* __restrict__ v_cache,
-                                                         const int64_t* __restrict__ pos, f16* __restrict__ out,
-                                                         int Hq, int Hkv, int L, float scale) {
+// out[m][h * D + d] = sum_j softmax_j(scale * q[m][h] . k[j]) v[j][d], KV head h / (Hq / Hkv) for query head h.
+// One block of W waves per (token, group of G consecutive query heads of one KV head): G = Hq / Hkv shares every K/V
+// read among the heads; G = 1 gives Hq / Hkv times more blocks (decode steps, where M Hkv blocks cannot fill the
+// chip). Lane l always owns dims 8 (l % 16) .. + 7 and key row-group l / 16: each 16-byte K and V load of a wave
+// reads four whole cache rows, the lane's slice of q stays in registers, a score is a 16-lane DPP sum, and the
+// probabilities never leave the lane that multiplies them into V. Waves take blocks of KB keys; the row groups and
+// the waves are merged at the end (lane shuffles, then LDS).
+template <int G, int KB>
+__global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ k_cache, const f16* __restrict__ v_cache,
+    const int64_t* __restrict__ pos, f16* __restrict__ out, int Hq, int Hkv, int L, float scale) {
+  constexpr int NI = KB / 4;                                 // 16-byte loads per lane and step, per K and per V
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int m = blockIdx.x / Hkv, hk = blockIdx.x % Hkv;
+  const int groups = Hq / G;
+  const int m = blockIdx.x / groups, h0 = (blockIdx.x % groups) * G, hk = h0 / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+  const int rg = lane >> 4, dl = (lane & 15) * 8;          // key row-group, first dim of the lane's slice
   const int64_t pm = pos[m];
-  const int nkeys = (int)min((int64_t)L, pm + 1);
-  // LDS: q [G][D] fp16 | p [W][G][64] fp32 | partial states [W][G] (max, sum) + [W][G][D] fp32
-  f16* qs = reinterpret_cast<f16*>(smem);
-  float* ps = reinterpret_cast<float*>(smem + G * kHeadDim * 2);
-  float* st = ps + W * G * 64;
-  float* os = st + W * G * 2;
-  for (int i = threadIdx.x; i < G * kHeadDim; i += blockDim.x)
-    qs[i] = q[((size_t)m * Hq + hk * G) * kHeadDim + i];
-  __syncthreads();
-
-  const f16* kb = k_cache + (size_t)hk * L * kHeadDim;
-  const f16* vb = v_cache + (size_t)hk * L * kHeadDim;
-  float mx[G], sum[G], o0[G], o1[G];
+  const int nkeys = (int)min((int64_t)L, pm + 1), last = nkeys - 1;
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const u32x4*>(q + ((size_t)m * Hq + h0 + g) * kHeadDim + dl);
+  const f16* kb = k_cache + (size_t)hk * L * kHeadDim + dl;
+  const f16* vb = v_cache + (size_t)hk * L * kHeadDim + dl;
+  float mx[G], sum[G], o[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     mx[g] = -INFINITY;
     sum[g] = 0.f;
-    o0[g] = o1[g] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[g][d] = 0.f;
   }
-  for (int base = wave * 64; base < nkeys; base += 64 * W) {
-    // scores: lane = key base + lane
-    const int j = base + lane;
-    float sc[G];
+  for (int base = wave * KB; base < nkeys; base += KB * W) {
+    // step keys base + 4 i + rg, i < NI (rows past the end are clamped and masked)
+    u32x4 kq[NI], vq[NI];
 #pragma unroll
-    for (int g = 0; g < G; ++g) sc[g] = 0.f;
-    if (j < nkeys) {
-      const u32x4* kr = reinterpret_cast<const u32x4*>(kb + (size_t)j * kHeadDim);
-#pragma unroll 4
-      for (int c = 0; c < kHeadDim / 8; ++c) {
-        const u32x4 kv = kr[c];
+    for (int i = 0; i < NI; ++i) kq[i] = *reinterpret_cast<const u32x4*>(kb + (size_t)min(base + 4 * i + rg, last) * kHeadDim);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const u32x4 qv = *reinterpret_cast<const u32x4*>(qs + g * kHeadDim + 8 * c);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sc[g] = dot2(as_f16x2(qv[e]), as_f16x2(kv[e]), sc[g]);
-        }
-      }
-    }
-    // online softmax over this block of keys, per head
+    for (int i = 0; i < NI; ++i) vq[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)min(base + 4 * i + rg, last) * kHeadDim);
+    __builtin_amdgcn_sched_barrier(0);                      // every load requested before the first is used
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float s = j < nkeys ? sc[g] * scale : -INFINITY;
-      const float bm = wave_max(s);
-      const float nm = fmaxf(mx[g], bm);
-      const float corr = expf(mx[g] - nm);                   // 0 on the first block (mx = -inf)
-      const float pj = j < nkeys ? expf(s - nm) : 0.f;
-      sum[g] = sum[g] * corr + wave_sum(pj);
-      o0[g] *= corr;
-      o1[g] *= corr;
-      mx[g] = nm;
-      ps[(wave * G + g) * 64 + lane] = pj;
-    }
-    __builtin_amdgcn_wave_barrier();                         // LDS is in order per wave; keep the compiler's order too
-    // P V: lane = output dims 2 lane, 2 lane + 1 (the wave reads back its own probabilities)
-    const int nb = min(64, nkeys - base);
-    for (int t = 0; t < nb; ++t) {
-      const f16x2 vv = *reinterpret_cast<const f16x2*>(vb + (size_t)(base + t) * kHeadDim + 2 * lane);
-      const float v0 = (float)vv[0], v1 = (float)vv[1];
+      float s[NI];
+      float bm = -INFINITY;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pj = ps[(wave * G + g) * 64 + t];
-        o0[g] = fmaf(pj, v0, o0[g]);
-        o1[g] = fmaf(pj, v1, o1[g]);
+      for (int i = 0; i < NI; ++i) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a = dot2(as_f16x2(qv[g][e]), as_f16x2(kq[i][e]), a);
+        a = row_sum(a) * scale;                              // the key's score, in all 16 lanes of the row group
+        s[i] = base + 4 * i + rg <= last ? a : -INFINITY;
+        bm = fmaxf(bm, s[i]);
       }
+      bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));                // the step's max over all its keys
+      const float nm = fmaxf(mx[g], bm);
+      const float corr = __expf(mx[g] - nm);                 // 0 on the first step (mx = -inf)
+      float ps = 0.f;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) o[g][d] *= corr;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const float pj = __expf(s[i] - nm);                  // 0 for masked keys
+        ps += pj;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 v2 = as_f16x2(vq[i][e]);
+          o[g][2 * e] = fmaf(pj, (float)v2[0], o[g][2 * e]);
+          o[g][2 * e + 1] = fmaf(pj, (float)v2[1], o[g][2 * e + 1]);
+        }
+      }
+      ps += __shfl_xor(ps, 16, 64);                           // + the other row groups' keys: the step's total
+      ps += __shfl_xor(ps, 32, 64);
+      sum[g] = sum[g] * corr + ps;
+      mx[g] = nm;
     }
-    __builtin_amdgcn_wave_barrier();                         // every lane has read ps before the next block rewrites it
   }
-  // merge the waves
+  // merge the four row groups (lanes l, l ^ 16, l ^ 32, l ^ 48 hold the same dims), then the waves through LDS
+  float* st = reinterpret_cast<float*>(smem);                // [W][G] (max, sum)
+  float* os = st + W * G * 2;                                // [W][G][D]
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      o[g][d] += __shfl_xor(o[g][d], 16, 64);
+      o[g][d] += __shfl_xor(o[g][d], 32, 64);
+    }
     if (lane == 0) {
       st[(wave * G + g) * 2] = mx[g];
       st[(wave * G + g) * 2 + 1] = sum[g];
     }
-    os[((wave * G + g) * kHeadDim) + 2 * lane] = o0[g];
-    os[((wave * G + g) * kHeadDim) + 2 * lane + 1] = o1[g];
+    if (rg == 0) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) os[(wave * G + g) * kHeadDim + dl + d] = o[g][d];
+    }
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
@@ -186,12 +192,12 @@ __global__ __launch_bounds__(1024) void attention_kernel(const f16* __restrict__
     float num = 0.f, den = 0.f;
     for (int w = 0; w < W; ++w) {
       const float wm = st[(w * G + g) * 2];
-      if (wm == -INFINITY) continue;                           // a wave that saw no key
+      if (wm == -INFINITY) continue;                          // a wave that saw no key
       const float f = expf(wm - gm);
       num = fmaf(f, os[(w * G + g) * kHeadDim + d], num);
       den = fmaf(f, st[(w * G + g) * 2 + 1], den);
     }
-    out[((size_t)m * Hq + hk * G + g) * kHeadDim + d] = (f16)(num / den);
+    out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
   }
 }
 
@@ -207,31 +213,29 @@ hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_f
 }
 
 namespace {
-template <int G>
+template <int G, int KB>
 hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
                             int Hkv, int L, int max_keys, float scale, hipStream_t st) {
-  int waves = 1;                                              // enough waves to give each about 64 keys
-  while (waves < 16 && waves * 64 < max_keys) waves *= 2;
-  const size_t lds = (size_t)G * kHeadDim * 2 + (size_t)waves * G * 64 * 4 + (size_t)waves * G * 2 * 4 +
-                     (size_t)waves * G * kHeadDim * 4;
-  if (lds > 65536) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<G>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
-    if (attr != hipSuccess) return attr;
-  }
-  return launch(attention_kernel<G>, dim3(M * Hkv), dim3(64 * waves), lds, st, q, k, v, pos, out, Hq, Hkv, L, scale);
+  const int max_waves = (G == 1 && KB == 32) ? 16 : 8;
+  int waves = 1;                                              // enough waves to give each one step of keys
+  while (waves < max_waves && waves * KB < max_keys) waves *= 2;
+  const size_t lds = (size_t)waves * G * 2 * 4 + (size_t)waves * G * kHeadDim * 4;
+  return launch(attention_kernel<G, KB>, dim3(M * (Hq / G)), dim3(64 * waves), lds, st, q, k, v, pos, out, Hq, Hkv,
+                L, scale);
 }
 }  // namespace
 
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
                             int Hkv, int L, int max_keys, float scale, hipStream_t st) {
+  if ((long)M * Hkv < 64)                                     // few tokens: one query head per block, short steps
+    return launch_attention<1, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
   switch (Hq / Hkv) {
-    case 1: return launch_attention<1>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 2: return launch_attention<2>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 4: return launch_attention<4>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 6: return launch_attention<6>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 7: return launch_attention<7>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 8: return launch_attention<8>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 1: return launch_attention<1, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 2: return launch_attention<2, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 4: return launch_attention<4, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 6: return launch_attention<6, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 7: return launch_attention<7, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 8: return launch_attention<8, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
     default: return hipErrorInvalidValue;
   }
 }
