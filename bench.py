@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--sweep", choices=["skinny"], default=None)
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
+    ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
+                    help="with --e2e MODEL: build only that variant, prefill, capture one step and replay --steps greedy "
+                         "tokens (a profiler workload; prints nothing else)")
     ap.add_argument("--out", default=None)
     return ap.parse_args()
 
@@ -484,6 +487,37 @@ def e2e(a):
         pathlib.Path(a.out).write_text(json.dumps(res, indent=1))
 
 
+def decode_trace(a):
+    """Profiler workload for one e2e variant: the model, the prompt prefill, one captured step, `steps` replays."""
+    import torch
+    from lowbit import decode, fused, model as lbmodel
+    cfg = E2E[a.e2e]
+    torch.cuda.set_device(0)
+    m = decode.random_model(a.e2e, seed=0)
+    steps = min(a.steps, 256)
+    max_len = cfg["prompt"] + steps + 64
+    clip = CLIP_GRID if cfg["clip"] else None
+    if a.decode_trace.startswith("fused"):
+        dec = fused.FusedDecoder(fused.FusedQwen2(m, max_len, quant=a.decode_trace.split("_")[1], clip_grid=clip))
+        del m
+    else:
+        if a.decode_trace == "hf_int4":
+            lbmodel.apply_int4(lbmodel.quantize_layers(m, GROUP, clip))
+        dec = decode.GraphDecoder(m, max_len, 1)
+    torch.cuda.empty_cache()
+    vocab = decode.qwen25_config(a.e2e).vocab_size
+    prompt = torch.randint(0, vocab, (1, cfg["prompt"]), generator=torch.Generator(device="cuda").manual_seed(2024),
+                           device="cuda")
+    first = dec.prefill(prompt).argmax(-1)
+    dec.capture()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.greedy(first, steps)
+    torch.cuda.synchronize()
+    print(json.dumps({"decode_trace": a.decode_trace, "e2e": a.e2e, "steps": steps,
+                      "ms_per_token": round(1000 * (time.perf_counter() - t0) / (steps - 1), 4)}), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -497,6 +531,8 @@ def main():
         pmc_workload(a)
     elif a.sweep == "skinny":
         sweep_skinny(a)
+    elif a.e2e and a.decode_trace:
+        decode_trace(a)
     elif a.e2e:
         e2e(a)
     else:
