@@ -115,10 +115,11 @@ int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int lay
  * otherwise the MFMA GEMM; workspace as for lowbit_w4_gemm_mfma). Each mode rounds as the unfused torch ops do
  * (the projection to fp16 first; silu in fp32 then fp16, the product fp16), so results equal the unfused sequence
  * (nn.Linear bias add of the reference's W4Linear, lowbit/model.py:25-26; the residual add and silu(gate) * up of
- * transformers' Qwen2 layer). */
+ * transformers' Qwen2 layer). norm_weight (may be NULL; M = 1 and K <= 16384 only): project
+ * lowbit_rmsnorm(x, norm_weight, eps) instead of x, the norm computed in the GEMV's prologue. */
 int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           int64_t group, int epilogue, const void* aux, const void* norm_weight, float eps,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* out[M][H] = weight * fp16(x / sqrt(mean(x^2) + eps)) (fp16 in/out, fp32 statistics; transformers Qwen2RMSNorm). */
 int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int64_t H, float eps, void* stream);

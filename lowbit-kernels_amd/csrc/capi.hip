@@ -220,8 +220,8 @@ int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int lay
 }
 
 int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
-                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
-                           void* stream) {
+                           int64_t group, int epilogue, const void* aux, const void* norm_weight, float eps,
+                           void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the fused projection takes 1..64 rows");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
@@ -233,11 +233,15 @@ int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y,
     return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
   if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
     return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
+  if (norm_weight && (M != 1 || K > 16384 || !aligned16(norm_weight)))
+    return fail(LOWBIT_ERR_ARG, "the fused input norm takes one row (M = 1), K <= 16384 and a 16-byte aligned weight");
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
              (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
   a.epi.mode = epilogue;
   a.epi.aux = static_cast<const f16*>(aux);
+  a.norm_w = static_cast<const f16*>(norm_weight);
+  a.eps = eps;
   return hip_status(M == 1 ? gemv_mfma_layout_launch(a, 0) : gemm_mfma_launch(a, 0, workspace, workspace_bytes),
                     "w4_linear_fused");
 }

@@ -54,8 +54,12 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
                                                                            f16* y, int N, int K, int G,
-                                                                           Epilogue epi) {
+                                                                           Epilogue epi,
+                                                                           const f16* __restrict__ norm_w, float eps) {
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
+  // norm_w (M = 1 with x in LDS only; the launcher then gives every block of x a thread): the projection's input is
+  // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
+  const bool norm = kLdsX && M == 1 && norm_w != nullptr;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int nb = M * (K / 32), ns = nrows * KG;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(ns * 2));
-  u32x4 xst[XB][4];
+  u32x4 xst[XB][4], wst[XB][4];
   if (kLdsX) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
@@ -82,6 +86,17 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       if (b < nb) {                                         // only threads that own a block issue its loads
 #pragma unroll
         for (int j = 0; j < 4; ++j) xst[u][j] = buffer_load16(xr, 64 * b + 16 * j);
+      }
+    }
+    if (norm) {
+      const __amdgpu_buffer_rsrc_t nr = make_rsrc(norm_w, (uint32_t)(K * 2));
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int b = (int)threadIdx.x + u * (int)blockDim.x;
+        if (b < nb) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) wst[u][j] = buffer_load16(nr, 64 * b + 16 * j);
+        }
       }
     }
   }
@@ -128,6 +143,44 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     lds_xs[2 * b] = lo;
     lds_xs[2 * b + 1] = hi;
   };
+  if (norm) {                                               // RMSNorm of the (single) row before staging it
+    __shared__ float ss_red[16];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      if (b < nb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 v = as_f16x2(xst[u][j][e]);
+            ss = fmaf((float)v[0], (float)v[0], ss);
+            ss = fmaf((float)v[1], (float)v[1], ss);
+          }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) ss_red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < nwaves; ++i) tot += ss_red[i];
+    const float rn = rsqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      if (b < nb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f16x2 v = as_f16x2(xst[u][j][e]), g = as_f16x2(wst[u][j][e]);
+            const f16x2 nv = {(f16)((float)v[0] * rn), (f16)((float)v[1] * rn)};
+            xst[u][j][e] = as_u32(f16x2{(f16)((float)g[0] * (float)nv[0]), (f16)((float)g[1] * (float)nv[1])});
+          }
+      }
+    }
+  }
   if (kLdsX) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
@@ -329,9 +382,10 @@ hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
   if (x_bytes + s_bytes <= kGemvLdsX)
     return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream,
-                  a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi);
+                  a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+  if (a.norm_w) return hipErrorInvalidValue;                 // the fused norm needs x in LDS (the C ABI checks K)
   return launch(gemv_mfma_layout<M, R, D, false>, grid, block, std::max(s_bytes, red_bytes), a.stream,
-                a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi);
+                a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
 }
 
 template <int M>
@@ -397,7 +451,11 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
 int pick_rows_rowmajor(int N, int M) { return N >= 512 ? 4 : (M >= 4 ? 2 : 1); }
 
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
-  const GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave);
+  GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave);
+  if (a.norm_w) {                                             // every 32-k block of x held by a thread (2 per thread)
+    const int need = (a.K / 32 + 127) / 128;
+    while (p.waves < need) p.waves *= 2;
+  }
   switch (a.M) {
     case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves, p.D);
     case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves, p.D);

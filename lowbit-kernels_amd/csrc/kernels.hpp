@@ -25,6 +25,8 @@ struct GemvArgs {
   int M, N, K, G;
   hipStream_t stream;
   Epilogue epi = {};
+  const f16* norm_w = nullptr;   // M = 1 GEMV only: project RMSNorm(x) * norm_w instead of x
+  float eps = 0.f;
 };
 
 struct GemvPlan {

@@ -30,8 +30,8 @@ SIGNATURES = {
     "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
-    "lowbit_w4_linear_fused": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp],
-                               _int),
+    "lowbit_w4_linear_fused": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_float, _vp,
+                                ctypes.c_size_t, _vp], _int),
     "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp], _int),
@@ -223,9 +223,10 @@ class NativeExt:
 
     # ---- decode-step fusions (lowbit_w4_linear_fused, lowbit_rmsnorm, lowbit_rope_kv, lowbit_attention) ----
 
-    def w4_linear_fused(self, x, w, s, group, epilogue, aux=None, out=None):
+    def w4_linear_fused(self, x, w, s, group, epilogue, aux=None, out=None, norm=None):
         """x [M, K] (M <= 64) times the MFMA-layout weight with the epilogue fused into the store; returns y
-        ([M, N], or [M, N / 2] for EPI_SILU_MUL). `out` may be given (for EPI_RESIDUAL it may be `aux` itself)."""
+        ([M, N], or [M, N / 2] for EPI_SILU_MUL). `out` may be given (for EPI_RESIDUAL it may be `aux` itself).
+        norm = (weight, eps), M = 1 only: project RMSNorm(x) * weight instead of x."""
         import torch
         _check_tensors(x, w, s, group)
         m, n = x.shape[0], w.shape[0]
@@ -238,8 +239,10 @@ class NativeExt:
         with _DeviceGuard(x.device):
             st = _stream(x.device)
             ws = workspace(x.device, st)
+            nw, eps = norm if norm is not None else (None, 0.0)
             check(self.lib.lowbit_w4_linear_fused(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group,
-                                                  int(epilogue), ptr(aux) if aux is not None else None, ptr(ws),
+                                                  int(epilogue), ptr(aux) if aux is not None else None,
+                                                  ptr(nw) if nw is not None else None, float(eps), ptr(ws),
                                                   ws.numel(), st))
         return y
 

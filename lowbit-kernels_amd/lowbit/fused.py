@@ -7,6 +7,8 @@ small launch costs ~3 us, that overhead, not the projections, dominates a decode
     rmsnorm -> qkv projection (+bias) -> rope + cache write -> attention -> o projection (+residual, in place)
     -> rmsnorm -> gate|up projection (silu(gate) * up) -> down projection (+residual, in place)
 
+(for one token with W4A16 projections the two RMSNorms run inside the q|k|v and gate|up GEMVs' prologues: 7 launches)
+
 with its own KV cache. The projections are either W4A16 (lowbit_w4_linear_fused: GEMV / MFMA kernels with the
 consumer fused into the store, for up to 64 rows; dequantize + hipBLASLt beyond) or fp16 (hipBLASLt through torch,
 bias and residual folded into addmm, silu * up as two torch ops), so the two variants share every other kernel and
@@ -40,10 +42,10 @@ class _W4:
         self.wq = ops.W4Weight(packed, scales, group, ("mma",), device=packed.device)
         self.bias = bias
 
-    def __call__(self, x, epilogue, aux=None, out=None):
+    def __call__(self, x, epilogue, aux=None, out=None, norm=None):
         wq = self.wq
         if x.shape[0] <= 64:
-            return ops.ext().w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out)
+            return ops.ext().w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out, norm)
         w = ops.dequant(wq)                                  # prefill: dequantize + hipBLASLt, epilogue in torch
         return _torch_epilogue(x, w, epilogue, aux, out)
 
@@ -54,7 +56,7 @@ class _F16:
     def __init__(self, weight, bias=None):
         self.w, self.bias = weight, bias
 
-    def __call__(self, x, epilogue, aux=None, out=None):
+    def __call__(self, x, epilogue, aux=None, out=None, norm=None):
         return _torch_epilogue(x, self.w, epilogue, aux, out)
 
 
@@ -132,15 +134,22 @@ class FusedQwen2:
         xn = torch.empty_like(h)
         q = torch.empty(m, self.hq, self.head_dim, dtype=torch.float16, device=h.device)
         attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
+        fuse = m == 1 and self.quant == "int4" and self.hidden <= 16384
         for i, lay in enumerate(self.layers):
-            ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
-            qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
+            if fuse:                                          # RMSNorm inside the projection's prologue
+                qkv = lay["qkv"](h, EPI_BIAS, lay["qkv"].bias, norm=(lay["in_norm"], self.eps))
+            else:
+                ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
+                qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
             ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
             ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
                           self.scale)
             lay["o"](attn, EPI_RESIDUAL, h, out=h)
-            ext.rmsnorm(h, lay["post_norm"], self.eps, out=xn)
-            act = lay["gu"](xn, EPI_SILU_MUL)
+            if fuse:
+                act = lay["gu"](h, EPI_SILU_MUL, norm=(lay["post_norm"], self.eps))
+            else:
+                ext.rmsnorm(h, lay["post_norm"], self.eps, out=xn)
+                act = lay["gu"](xn, EPI_SILU_MUL)
             lay["down"](act, EPI_RESIDUAL, h, out=h)
         ext.rmsnorm(h, self.final_norm, self.eps, out=xn)
         return F.linear(xn, self.head)

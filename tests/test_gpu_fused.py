@@ -46,6 +46,26 @@ def test_epilogues_equal_the_unfused_ops(cuda, k, n):
         assert ulp_diff(got, want) <= 1 and float((got != want).float().mean()) < 0.01, m
 
 
+@pytest.mark.parametrize("k,n", [(256, 512), (1536, 2048), (2048, 22016), (3584, 4608)])
+def test_fused_input_norm_matches_norm_then_projection(cuda, k, n):
+    wq, _, *_, gen = make_weight(k, n, 3 * k + n, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    nw = (1 + 0.1 * torch.randn(k, generator=gen)).half().cuda()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    for scale in (1.0, 40.0, 1e-3):
+        x = (torch.randn(1, k, generator=gen) * scale).half().cuda()
+        want = ext.w4_linear_fused(ext.rmsnorm(x, nw, 1e-6), wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias)
+        got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias, norm=(nw, 1e-6))
+        assert rel(got, want.double()) < 2e-3, (k, n, scale)
+        if n % 16 == 0:
+            want = ext.w4_linear_fused(ext.rmsnorm(x, nw, 1e-6), wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL)
+            got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL, norm=(nw, 1e-6))
+            assert rel(got, want.double()) < 2e-3, (k, n, scale)
+    with pytest.raises(RuntimeError, match="one row"):
+        x2 = torch.randn(2, k, generator=gen).half().cuda()
+        ext.w4_linear_fused(x2, wq.packed_mma, wq.scales, wq.group, fused.EPI_STORE, norm=(nw, 1e-6))
+
+
 def test_rmsnorm_matches_qwen2_rmsnorm(cuda):
     from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
     g = torch.Generator().manual_seed(1)
@@ -127,15 +147,21 @@ def test_fused_qwen2_matches_transformers(cuda, tiny_models):
     err = float((got - ref).abs().max() / ref.pow(2).mean().sqrt())
     assert err < 2e-2, err
     assert float((got.argmax(-1) == ref.argmax(-1)).float().mean()) >= 0.9
-    # int4: same quantized weights as lowbit.model's W4Linear path (fake-quant reference in torch)
+    # int4: same quantized weights as lowbit.model's W4Linear path (fake-quant reference in torch); 16 tokens per step
+    # (MFMA projections, separate RMSNorm) and one (GEMV with the RMSNorm in its prologue)
     q4 = fused.FusedQwen2(m, 128, quant="int4")
     d4 = fused.FusedDecoder(q4, chunk=16)
     d4.prefill(prompt)
     d4.capture()
     got4 = d4.step(feed).float()
+    d1 = fused.FusedDecoder(q4, chunk=1)
+    d1.prefill(prompt)
+    d1.capture()
+    got1 = torch.cat([d1.step(feed[i:i + 1]).float().clone() for i in range(16)])
     layers = lbmodel.quantize_layers(m, 128)
     lbmodel.apply_fake_quant(layers)
     with torch.inference_mode():
         ref4 = m(torch.cat([prompt[0], feed]).view(1, -1)).logits[0, 70:].float()
-    err4 = float((got4 - ref4).abs().max() / ref4.pow(2).mean().sqrt())
-    assert err4 < 2e-2, err4
+    for got in (got4, got1):
+        err4 = float((got - ref4).abs().max() / ref4.pow(2).mean().sqrt())
+        assert err4 < 2e-2, err4
