@@ -37,7 +37,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per GEMV launch of this workload, measured: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
 # `bench.py --pmc-workload` (20 eager steps), each scaled by what the counter reads for a 1 GiB elementwise copy in the
 # same run (FETCH x2.0, WRITE x1.0); 1.03x the algorithmic bytes. Re-measure when the kernel changes.
-TRAFFIC_PER_LAUNCH = 4712920
+TRAFFIC_PER_LAUNCH = 4713005
 MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
 
 
@@ -259,7 +259,7 @@ def contract(a):
         # the timed graph holds only the M=1 GEMV kernel, so its average launch duration is elapsed / launches
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_PER_LAUNCH,
-                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true>",
+                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false>",
                      "kernel_avg_us": round(1000 * elapsed_ms / launches, 3), "launches": launches,
                      "bytes_per_launch_avg": step_bytes // len(projs)},
         "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,

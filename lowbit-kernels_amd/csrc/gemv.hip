@@ -49,7 +49,7 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 // refilled as soon as it is consumed. Weight loads use one buffer resource per tile: chunks past K and rows past N
 // read as zero without a branch, so the compiler waits on exactly the slot it needs. When M K is too large for LDS
 // (kLdsX = false) each lane loads its x pairs from global memory and decodes exactly.
-template <int M, int R, int D, bool kLdsX>
+template <int M, int R, int D, bool kLdsX, bool kFused = false>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   // norm_w (M = 1 with x in LDS only; the launcher then gives every block of x a thread): the projection's input is
   // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
-  const bool norm = kLdsX && M == 1 && norm_w != nullptr;
+  const bool norm = kFused && kLdsX && M == 1 && norm_w != nullptr;   // kFused: epilogue / norm code compiled in
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -282,11 +282,11 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       for (int m = 0; m < M; ++m) {
         const float v = quad_sum(acc[i][m]);
         const int n = 16 * (t0 + i) + r;
-        if (epi.mode == kEpiSiluMul) {                      // row r + 8 (the up row) sits 32 lanes on
+        if (kFused && epi.mode == kEpiSiluMul) {            // row r + 8 (the up row) sits 32 lanes on
           const float up = shfl_down32(v);
           if (q == 0 && r < 8 && n < N) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
         } else if (q == 0 && n < N) {
-          y[(size_t)m * N + n] = epi_value(epi.mode, epi.aux, v, m, n, N);
+          y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
         }
       }
     return;
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   for (int idx = threadIdx.x; idx < R * M * 16; idx += blockDim.x) {
     const int i = idx / (M * 16), m = (idx / 16) % M, rr = idx % 16;
     const int n = 16 * (t0 + i) + rr;
-    if (epi.mode == kEpiSiluMul) {
+    if (kFused && epi.mode == kEpiSiluMul) {
       if (rr >= 8 || n >= N) continue;
       float g = 0.f, u = 0.f;
       for (int wv2 = 0; wv2 < nwaves; ++wv2) {
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
     float v = 0.f;
     for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * 16) + idx];
-    if (n < N) y[(size_t)m * N + n] = epi_value(epi.mode, epi.aux, v, m, n, N);
+    if (n < N) y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
   }
 }
 
@@ -380,10 +380,22 @@ hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const size_t s_bytes = (size_t)16 * R * (a.K / a.G) * 2;
   const size_t x_bytes = (size_t)M * a.K * 2 + (size_t)M * (a.K / 32) * 8;
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
+  const bool fused = a.epi.mode != kEpiStore || a.norm_w;
+  if constexpr (M == 1) {                                    // only the M = 1 path carries epilogues and the norm
+    if (fused) {
+      if (x_bytes + s_bytes <= kGemvLdsX)
+        return launch(gemv_mfma_layout<M, R, D, true, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes),
+                      a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+      if (a.norm_w) return hipErrorInvalidValue;             // the fused norm needs x in LDS (the C ABI checks K)
+      return launch(gemv_mfma_layout<M, R, D, false, true>, grid, block, std::max(s_bytes, red_bytes), a.stream,
+                    a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+    }
+  } else {
+    if (fused) return hipErrorInvalidValue;                   // callers send M >= 2 with an epilogue to the MFMA GEMM
+  }
   if (x_bytes + s_bytes <= kGemvLdsX)
     return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream,
                   a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
-  if (a.norm_w) return hipErrorInvalidValue;                 // the fused norm needs x in LDS (the C ABI checks K)
   return launch(gemv_mfma_layout<M, R, D, false>, grid, block, std::max(s_bytes, red_bytes), a.stream,
                 a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
 }
