@@ -16,8 +16,11 @@ x K / elapsed, in GB/s: whole-job throughput including the per-kernel launch gap
 roofline = the GEMV kernel: the timed graph holds only its launches, so its average launch duration is elapsed /
 (14 K) and achieved = the same bytes / that time; peak = 8 TB/s (MI355X HBM3E). per_shape: each distinct (K, N) alone,
 per call in a graph over >= 1 GiB of copies.
+measured_peak = HBM read and copy bandwidth over a 2 GiB buffer, by the reference's torch method and by the library's
+streaming probes; per_shape also gives each layer's share of the measured read peak.
 cpu_baseline = the reference's CPU path (oracle: dequantize to fp16, then torch.nn.functional.linear on the host) on a
-bounded sample of the same steps.
+bounded sample of the same steps, plus the per-call breakdown at BASELINE configs[0] (quantize, dequantize + linear,
+linear alone; all torch threads and one).
 """
 import argparse
 import json
@@ -125,7 +128,97 @@ def cpu_baseline(projs, host, xs, budget_s=15.0):
     return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{steps} steps of the same 14-projection M=1 sweep ({step_bytes / 1e6:.1f} MB each): oracle "
                       f"dequant to fp16 + torch.nn.functional.linear on {threads} host threads, {el:.1f} s",
-            "ms_per_step": round(1000 * el / steps, 3)}
+            "ms_per_step": round(1000 * el / steps, 3), "config1": cpu_breakdown()}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_breakdown(k=896, n=4864, rounds=5):
+    """BASELINE configs[0] on the host: M=1, K=896, N=4864, weights N(0, 0.02), x N(0, 1) fp16, absmax g128. Median
+    seconds per call (after one warm-up) of (i) dequantize to fp16 + torch linear, (ii) torch linear on the
+    pre-dequantized fp16 weight, (iii) quantize (one-off), with torch on all its threads and on one; the oracle's
+    numpy steps are single-threaded either way. The fp64 error of the result is reported beside."""
+    import numpy as np
+    import torch
+    from oracle import quant_ref as R
+    rng = np.random.default_rng(k * 7 + n)                  # the reference's seed rule, bench/gpu_run.py:206
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float16))
+    packed, scales = R.quantize_w4(w, GROUP)
+    w16 = torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP))
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(rounds):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return round(sorted(ts)[len(ts) // 2] * 1e3, 3)
+
+    full = torch.get_num_threads()
+    out = {"shape": {"M": 1, "K": k, "N": n, "group": GROUP}, "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+           "torch_threads": full, "unit": "ms per call (median of %d)" % rounds}
+    for threads in (full, 1):
+        torch.set_num_threads(threads)
+        out[f"threads_{threads}"] = {
+            "dequant_linear_ms": med(lambda: torch.nn.functional.linear(
+                x, torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP)))),
+            "linear_only_ms": med(lambda: torch.nn.functional.linear(x, w16)),
+            "quantize_ms": med(lambda: R.quantize_w4(w, GROUP))}
+    torch.set_num_threads(full)
+    y = torch.nn.functional.linear(x, w16).numpy()
+    out["rel_err_vs_fp64"] = R.rel_err(y, R.gemv_reference(x.double().numpy(), packed, scales, GROUP))
+    return out
+
+
+def measured_peak(torch, ops, gib=2):
+    """HBM bandwidth over a `gib` GiB buffer, two ways. The reference's method (bench/gpu_run.py:133-141, there over
+    256 MiB): torch's device copy (read + write every byte) and torch's sum (read). And this library's streaming
+    probes (lowbit_hbm_read / lowbit_hbm_copy), swept over grid sizes. Each figure is the best of 3 timed rounds of
+    5 calls after one warm-up; read_gbps = the best read figure of either method is the roofline's measured peak."""
+    e = ops.ext()
+    n = gib * 2 ** 30 // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nbytes = n * 4
+
+    def best_gbps(fn, moved):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        best = 1e30
+        for _ in range(3):
+            e0.record()
+            for _ in range(5):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) / 5)
+        return round(moved / (best * 1e-3) / 1e9, 1)
+
+    out = {"bytes": nbytes,
+           "torch_copy_gbps": best_gbps(lambda: dst.copy_(src), 2 * nbytes),
+           "torch_sum_gbps": best_gbps(lambda: src.sum(), nbytes)}
+    reads, copies = {}, {}
+    for blocks in (512, 1024, 2048, 4096, 8192):
+        reads[blocks] = best_gbps(lambda: e.hbm_read(src, sink, blocks), nbytes)
+        copies[blocks] = best_gbps(lambda: e.hbm_copy(src, dst, blocks), 2 * nbytes)
+    out["probe_read_gbps"], out["probe_copy_gbps"] = reads, copies
+    out["read_gbps"] = max(max(reads.values()), out["torch_sum_gbps"])
+    out["copy_gbps"] = max(max(copies.values()), out["torch_copy_gbps"])
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
 
 
 def graph_time_us(torch, fn, iters, reps=3):
@@ -150,8 +243,9 @@ def graph_time_us(torch, fn, iters, reps=3):
     return best
 
 
-def shape_detail(torch, ops, projs, pool, xs):
-    """Per distinct (K, N): M=1 ops.linear per call in a hipGraph over >= 1 GiB of copies of that layer."""
+def shape_detail(torch, ops, projs, pool, xs, peak=None):
+    """Per distinct (K, N): M=1 ops.linear per call in a hipGraph over >= 1 GiB of copies of that layer; its share of
+    8 TB/s and of the measured read peak `peak` (GB/s)."""
     out = {}
     seen = set()
     for name, k, n in projs:
@@ -172,6 +266,8 @@ def shape_detail(torch, ops, projs, pool, xs):
         out[f"{k}x{n}"] = {"us_per_call": round(us, 2), "GBps": round(alg_bytes(k, n) / (us * 1e-6) / 1e9, 1),
                            "pct_of_8TBps": round(100 * alg_bytes(k, n) / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 1),
                            "copies": copies}
+        if peak:
+            out[f"{k}x{n}"]["pct_of_measured_peak"] = round(100 * alg_bytes(k, n) / (us * 1e-6) / 1e9 / peak, 1)
         del cl
         torch.cuda.empty_cache()
     return out
@@ -237,7 +333,8 @@ def contract(a):
             for name, k, n in projs:
                 torch.nn.functional.linear(xs[name], layer[name])
         fp16 = graph_time_us(torch, step16, a.steps, reps=1) / 1000
-    detail = None if a.no_detail else shape_detail(torch, ops, projs, pool, xs)
+    peak = None if a.no_detail else measured_peak(torch, ops)
+    detail = None if a.no_detail else shape_detail(torch, ops, projs, pool, xs, peak["read_gbps"])
 
     line = {
         "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1; us/call M=1..64 vs hipBLASLt fp16",
@@ -265,8 +362,12 @@ def contract(a):
         "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,
         "speedup_vs_fp16_blas": round(fp16 / (elapsed_ms / a.steps), 3) if fp16 else None,
         "blas_backend": str(torch.backends.cuda.preferred_blas_library()),
+        "measured_peak": peak,
         "per_shape": detail,
     }
+    if peak:
+        line["roofline"]["measured_peak_gbps"] = peak["read_gbps"]
+        line["roofline"]["frac_of_measured_peak"] = round(value / peak["read_gbps"], 4)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(projs, host, xs)
     print(json.dumps(line), flush=True)

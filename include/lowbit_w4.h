@@ -136,6 +136,14 @@ int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_f
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* stream);
 
+/* ---- HBM bandwidth probes (the measured peak that kernel bandwidths are quoted against) ----
+ * The reference measures its peak with a torch device copy and a torch sum over 256 MiB (bench/gpu_run.py:133-141);
+ * these are streaming kernels of this library for the same two figures. hbm_read reads `bytes` (a multiple of 16,
+ * 16-byte aligned source) with 16-byte loads over `blocks` workgroups of 256 threads and writes at most one 32-bit
+ * word to `sink`; hbm_copy copies `bytes` from src to dst. */
+int lowbit_hbm_read(const void* src, int64_t bytes, void* sink, int64_t blocks, void* stream);
+int lowbit_hbm_copy(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream);
+
 /* ---- host-side format functions (CPU memory, no GPU needed); counterparts of lowbit/quant.py ---- */
 
 /* quant.quantize_w4 (lowbit/quant.py:23-35): w float32 [N, K] -> packed [N, K/2], scales fp16 bits [N, K/G]. */

@@ -285,4 +285,24 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
                     "attention");
 }
 
+int lowbit_hbm_read(const void* src, int64_t bytes, void* sink, int64_t blocks, void* stream) {
+  if (!src || !sink) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (bytes < 16 || bytes % 16) return fail(LOWBIT_ERR_SHAPE, "hbm_read: bytes must be a positive multiple of 16");
+  if (blocks < 1 || blocks > 65536) return fail(LOWBIT_ERR_SHAPE, "hbm_read: blocks must be 1..65536");
+  if (!aligned16(src) || reinterpret_cast<uintptr_t>(sink) % 4) return fail(LOWBIT_ERR_ALIGN, "hbm_read needs a 16-byte aligned source");
+  if (int rc = check_device()) return rc;
+  return hip_status(hbm_read_launch(src, (size_t)bytes, static_cast<uint32_t*>(sink), (int)blocks,
+                                    static_cast<hipStream_t>(stream)),
+                    "hbm_read");
+}
+
+int lowbit_hbm_copy(const void* src, void* dst, int64_t bytes, int64_t blocks, void* stream) {
+  if (!src || !dst) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (bytes < 16 || bytes % 16) return fail(LOWBIT_ERR_SHAPE, "hbm_copy: bytes must be a positive multiple of 16");
+  if (blocks < 1 || blocks > 65536) return fail(LOWBIT_ERR_SHAPE, "hbm_copy: blocks must be 1..65536");
+  if (!aligned16(src) || !aligned16(dst)) return fail(LOWBIT_ERR_ALIGN, "hbm_copy needs 16-byte aligned buffers");
+  if (int rc = check_device()) return rc;
+  return hip_status(hbm_copy_launch(src, dst, (size_t)bytes, (int)blocks, static_cast<hipStream_t>(stream)), "hbm_copy");
+}
+
 }  // extern "C"

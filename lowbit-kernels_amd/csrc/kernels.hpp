@@ -87,6 +87,8 @@ hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, s
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st);
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
                           f16* v_cache, int M, int Hq, int Hkv, int L, hipStream_t st);
+hipError_t hbm_read_launch(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t stream);
+hipError_t hbm_copy_launch(const void* src, void* dst, size_t bytes, int blocks, hipStream_t stream);
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
                             int Hkv, int L, int max_keys, float scale, hipStream_t st);
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st);

@@ -35,6 +35,8 @@ SIGNATURES = {
     "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp], _int),
+    "lowbit_hbm_read": ([_vp, _i64, _vp, _i64, _vp], _int),
+    "lowbit_hbm_copy": ([_vp, _vp, _i64, _i64, _vp], _int),
     "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
     "lowbit_host_unpack": ([_vp, _vp, _i64, _i64], _int),
     "lowbit_host_dequantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
@@ -264,3 +266,18 @@ class NativeExt:
             check(self.lib.lowbit_attention(ptr(q), ptr(k_cache), ptr(v_cache), ptr(positions), ptr(out), q.shape[0],
                                             hq, hkv, k_cache.shape[1], int(max_keys), float(scale),
                                             _stream(q.device)))
+
+    # ---- bandwidth probes (lowbit_hbm_read, lowbit_hbm_copy) ----
+    def hbm_read(self, buf, sink, blocks):
+        """Stream every byte of the contiguous CUDA tensor `buf` (nbytes a multiple of 16) through `blocks`
+        workgroups; `sink` is a CUDA int32 tensor the kernel may write one word to."""
+        with _DeviceGuard(buf.device):
+            check(self.lib.lowbit_hbm_read(ptr(buf), buf.numel() * buf.element_size(), ptr(sink), int(blocks),
+                                           _stream(buf.device)))
+
+    def hbm_copy(self, src, dst, blocks):
+        if src.numel() * src.element_size() != dst.numel() * dst.element_size():
+            raise RuntimeError("hbm_copy: src and dst must have the same size in bytes")
+        with _DeviceGuard(src.device):
+            check(self.lib.lowbit_hbm_copy(ptr(src), ptr(dst), src.numel() * src.element_size(), int(blocks),
+                                           _stream(src.device)))

@@ -58,6 +58,12 @@ def _msg(rc):
     (lambda l: l.lowbit_set_launch_override(3, 0, 0), 8, "waves_per_group"),
     (lambda l: l.lowbit_set_launch_override(4, 5, 0), 8, "ring"),
     (lambda l: l.lowbit_set_launch_override(4, 4, 33), 8, "k_splits"),
+    (lambda l: l.lowbit_hbm_read(None, 1024, FAKE, 256, None), 1, "null pointer"),
+    (lambda l: l.lowbit_hbm_read(FAKE, 1000, FAKE, 256, None), 3, "multiple of 16"),
+    (lambda l: l.lowbit_hbm_read(FAKE, 1024, FAKE, 0, None), 3, "blocks"),
+    (lambda l: l.lowbit_hbm_read(ctypes.c_void_p(4100), 1024, FAKE, 256, None), 4, "16-byte"),
+    (lambda l: l.lowbit_hbm_copy(FAKE, FAKE, 0, 256, None), 3, "multiple of 16"),
+    (lambda l: l.lowbit_hbm_copy(FAKE, FAKE, 1024, 70000, None), 3, "blocks"),
 ])
 def test_validation_refuses_before_any_gpu_call(call, code, text):
     rc = call(_native.lib())

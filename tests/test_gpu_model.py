@@ -87,3 +87,39 @@ def test_greedy_graph_decode_runs_on_device(cuda, models):
             eager.append(int(dec2._forward()[-1].argmax(-1)))
         dec2.pos += 1
     assert toks.tolist() == eager
+
+
+def test_saved_int4_loads_to_the_same_model(cuda, tmp_path):
+    """quantize once, save_int4, load_int4 into a fresh copy of the model: the same W4Linear weights and bit-identical
+    logits, with no quantizer call; a file whose shapes do not fit the model is refused."""
+    from lowbit import store
+    a = decode.random_model("tiny", seed=12)
+    b = decode.random_model("tiny", seed=12)
+    layers = lbmodel.quantize_layers(a, 128, CLIP)
+    path = tmp_path / "tiny_int4.safetensors"
+    lbmodel.save_int4(a, layers, path, 128, CLIP)
+    assert store.read_meta(path)["clip_grid"] == CLIP
+    ra, na = lbmodel.apply_int4(layers)
+    rb, nb = lbmodel.load_int4(b, path)
+    assert (ra, na) == (rb, nb) == (14, na)
+    for la, lb in zip(a.model.layers, b.model.layers):
+        for qa, qb in ((la.self_attn.q_proj, lb.self_attn.q_proj), (la.mlp.down_proj, lb.mlp.down_proj)):
+            assert torch.equal(qa.wq.packed_mma, qb.wq.packed_mma) and torch.equal(qa.wq.scales, qb.wq.scales)
+    ids = torch.randint(0, 1024, (1, 37), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda")
+    with torch.inference_mode():
+        assert torch.equal(a(ids).logits, b(ids).logits)
+    # a file from a model of another shape: same names, other widths
+    ents, g = store.load_w4(path)
+    name = "model.layers.0.mlp.up_proj"
+    p, s = ents[name]
+    ents[name] = (p[:256].contiguous(), s[:256].contiguous())
+    bad = tmp_path / "bad.safetensors"
+    store.save_w4(bad, ents, g)
+    c = decode.random_model("tiny", seed=12)
+    with pytest.raises(ValueError, match="saved weight is 256 x 256"):
+        lbmodel.load_int4(c, bad)
+    assert not any(isinstance(mod, lbmodel.W4Linear) for mod in c.modules())      # nothing was swapped
+    del ents[name]
+    store.save_w4(bad, ents, g)
+    with pytest.raises(KeyError, match="no entry"):
+        lbmodel.load_int4(decode.random_model("tiny", seed=12), bad)
