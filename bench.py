@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]        # the contract line
     python bench.py --sweep skinny [--out FILE]                # M = 1..64, three ways
+    python bench.py --sweep prefill [--out FILE]               # M = 128..2048: dequant + BLAS vs the int4 GEMM
     python bench.py --no-cpu --steps 50                        # shorter run (profiling)
 
 Workload (the M=1 GEMV sweep over the Qwen2.5-1.5B and 3B decoder projections): one step is an
@@ -71,7 +72,7 @@ def parse():
     ap.add_argument("--no-detail", action="store_true", help="skip the per-shape timings")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny"], default=None)
+    ap.add_argument("--sweep", choices=["skinny", "prefill"], default=None)
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
@@ -426,6 +427,41 @@ def sweep_skinny(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+def sweep_prefill(a):
+    """Prefill, M in {128, 512, 2048} on the Qwen2.5-3B layer (merged q|k|v and gate|up, o, down) and the 7B MLP
+    projections: us/call of dequantize + hipBLASLt, fp16 hipBLASLt, the int4 prefill GEMM (automatic launch plan) and
+    linear() (auto route), each a graph cycling >= 1 GiB of int4 copies (fp16: >= 1 GiB of fp16 copies)."""
+    import torch
+    from lowbit import ops
+    torch.cuda.set_device(0)
+    shapes = [("3b.qkv", 2048, 2560), ("3b.o", 2048, 2048), ("3b.gate_up", 2048, 22016), ("3b.down", 11008, 2048),
+              ("7b.gate_up", 3584, 18944), ("7b.down", 18944, 3584)]
+    rows = []
+    for name, k, n in shapes:
+        projs = [(name, k, n)]
+        pool, pool16, _, copies = build_pool(torch, ops, projs, fp16=True, seed=k + n)
+        e = ops.ext()
+        for m in (128, 512, 2048):
+            x = torch.randn(m, k, device="cuda").half()
+            r = {"shape": name, "K": k, "N": n, "M": m, "copies": copies}
+            it = max(40, copies)
+            r["dequant_blas_us"] = round(graph_time_us(torch, lambda i: torch.nn.functional.linear(
+                x, ops.dequant(pool[i % copies][name], "mma")), it), 2)
+            r["fp16_blas_us"] = round(graph_time_us(torch, lambda i: torch.nn.functional.linear(
+                x, pool16[i % copies][name]), it), 2)
+            r["int4_prefill_us"] = round(graph_time_us(torch, lambda i: ops.prefill(x, pool[i % copies][name]), it), 2)
+            r["linear_us"] = round(graph_time_us(torch, lambda i: ops.linear(x, pool[i % copies][name]), it), 2)
+            r["linear_path"] = "prefill" if ops.prefill_path(m, pool[0][name]) else "dequant+blas"
+            r["int4_prefill_tflops"] = round(2 * m * n * k / (r["int4_prefill_us"] * 1e-6) / 1e12, 1)
+            r["fp16_blas_tflops"] = round(2 * m * n * k / (r["fp16_blas_us"] * 1e-6) / 1e12, 1)
+            rows.append(r)
+            print(json.dumps(r), flush=True)
+        del pool, pool16
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
 def pmc_workload(a):
     """For rocprofv3 --pmc: one elementwise copy of exactly 1 GiB (read 1 GiB, write 1 GiB: the calibration of
     FETCH_SIZE / WRITE_SIZE), then a.steps eager steps of the contract workload (14 GEMV launches each)."""
@@ -632,6 +668,8 @@ def main():
         pmc_workload(a)
     elif a.sweep == "skinny":
         sweep_skinny(a)
+    elif a.sweep == "prefill":
+        sweep_prefill(a)
     elif a.e2e and a.decode_trace:
         decode_trace(a)
     elif a.e2e:

@@ -121,6 +121,17 @@ int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y,
                            int64_t group, int epilogue, const void* aux, const void* norm_weight, float eps,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* Prefill GEMM, any M >= 1 (meant for M > 64): y [M, N] = x [M, K] . dequant(W)^T on the MFMA layout (K and group
+ * multiples of 128), reading the int4 weights directly, with the same epilogues as lowbit_w4_linear_fused. Replaces
+ * the reference's prefill path, dequantize to fp16 + cuBLAS (lowbit/ops.py:126-135,163-178): the weights multiplied
+ * are exactly the dequantized fp16 values. The workspace (optional, as for lowbit_w4_gemm_mfma: counters zeroed before
+ * the first call and left zero) lets K split across workgroups when the tiles alone do not fill the GPU; partial sums
+ * take S * M * N * 4 bytes after the counters, and the split count is lowered to what fits. Requires
+ * (M + 128) * K * 2 < 2^31. */
+int lowbit_w4_gemm_prefill(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* out[M][H] = weight * fp16(x / sqrt(mean(x^2) + eps)) (fp16 in/out, fp32 statistics; transformers Qwen2RMSNorm). */
 int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int64_t H, float eps, void* stream);
 

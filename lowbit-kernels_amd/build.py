@@ -18,7 +18,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 OUT = PKG / "lowbit" / "liblowbit_w4.so"
-SOURCES = ["capi.hip", "gemv.hip", "gemm_mfma.hip", "dequant.hip", "quantize.hip", "decode_ops.hip", "hbm_probe.hip",
+SOURCES = ["capi.hip", "gemv.hip", "gemm_mfma.hip", "gemm_prefill.hip", "dequant.hip", "quantize.hip", "decode_ops.hip", "hbm_probe.hip",
            "host_format.cpp"]
 ARCH = "gfx950"
 # packed-fp32 ops stay off: only scalar fp32 and packed fp16 arithmetic is emitted

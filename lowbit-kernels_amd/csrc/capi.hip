@@ -177,6 +177,7 @@ int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_
   if (!aligned16(out)) return fail(LOWBIT_ERR_ALIGN, "the output must be 16-byte aligned");
   if (mfma_layout && (K % 128 || group % 128))
     return fail(LOWBIT_ERR_LAYOUT, "the v5 layout needs K and group % 128 == 0");
+  if (N * (K / 8) >= (int64_t{1} << 32) - 1024) return fail(LOWBIT_ERR_SHAPE, "dequant takes N * K < 2^35");
   if (int rc = check_device()) return rc;
   return hip_status(dequant_launch(static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(out),
                                    (int)N, (int)K, (int)group, mfma_layout != 0, static_cast<hipStream_t>(stream)),
@@ -244,6 +245,29 @@ int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y,
   a.eps = eps;
   return hip_status(M == 1 ? gemv_mfma_layout_launch(a, 0) : gemm_mfma_launch(a, 0, workspace, workspace_bytes),
                     "w4_linear_fused");
+}
+
+int lowbit_w4_gemm_prefill(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                           int64_t group, int epilogue, const void* aux, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
+  if (M < 1) return fail(LOWBIT_ERR_ROWS, "the prefill GEMM takes at least one row");
+  if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
+  if (int rc = check_mfma_layout_limits(N, K, group, false)) return rc;
+  if ((M + 128) * K * 2 > INT_MAX) return fail(LOWBIT_ERR_SHAPE, "the prefill GEMM takes (M + 128) * K * 2 < 2^31");
+  if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
+  if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
+    return fail(LOWBIT_ERR_ARG, "the bias and residual epilogues need aux");
+  if (epilogue == LOWBIT_EPI_SILU_MUL && (N % 16 || (reinterpret_cast<uintptr_t>(y) & 7)))
+    return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
+  if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
+    return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
+  a.epi.mode = epilogue;
+  a.epi.aux = static_cast<const f16*>(aux);
+  return hip_status(gemm_prefill_launch(a, workspace, workspace_bytes), "w4_gemm_prefill");
 }
 
 int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int64_t H, float eps, void* stream) {

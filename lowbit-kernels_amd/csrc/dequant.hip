@@ -1,9 +1,9 @@
 // Dequantize to fp16 W [N, K] (the prefill path's first half, then hipBLASLt), and the device relayout
 // canonical -> v3 / MFMA layouts.
 //
-// Dequant: each thread owns one 16-byte piece of packed weights (32 values of one row, inside one group because
-// G % 32 == 0) and writes its 64 output bytes with four 16-byte stores; consecutive threads write consecutive output
-// (row-major), so a wave writes 4 KB contiguous. The value is (u - 8) exactly in fp16 (magic-number decode) times
+// Dequant: each thread decodes 4 packed words (8 values of one row each, inside one group because G % 32 == 0) and
+// writes each as one 16-byte store; consecutive threads own consecutive words, so loads and stores are contiguous
+// per instruction. The value is (u - 8) exactly in fp16 (magic-number decode) times
 // the fp16 scale with one IEEE rounding: bit-identical to float16((u - 8) * scale) computed in fp64, which is the
 // reference rule (csrc/w4_gemv.cu:296-310,393-408; checked bit for bit at bench/gpu_run.py:217-228).
 #include "kernels.hpp"
@@ -29,33 +29,49 @@ __device__ __forceinline__ size_t mfma_offset(int n, int c, int q, int N, int K)
 
 }  // namespace
 
+// A piece is 8 consecutive outputs of one row: one 4-byte packed word in, 16 bytes out, and piece p of the
+// row-major output starts at element 8p. A workgroup owns 1024 consecutive pieces, 4 per thread spaced 256 apart, so
+// every load instruction reads and every store instruction writes a contiguous span (1 KB / 4 KB per workgroup).
+// All 4 loads of a thread are issued before the first decode.
 template <bool kMfma>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w, const f16* __restrict__ s,
                                                       f16* __restrict__ out, int N, int K, int G) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x, per_row = (size_t)K / 32;
-  if (idx >= (size_t)N * per_row) return;
-  const int n = (int)(idx / per_row), b = (int)(idx % per_row);     // output k = 32 b .. 32 b + 31
-  const size_t src = kMfma ? mfma_offset(n, b >> 2, b & 3, N, K) : idx * 16;
-  const u32x4 wv = load_stream(w + src);
-  const f16 sv = s[(size_t)n * (K / G) + (32 * b) / G];
-  const f16x2 sc = {sv, sv};
-  u32x4 o[4];
+  const uint32_t per_row = (uint32_t)K / 8, total = (uint32_t)N * per_row, groups = (uint32_t)(K / G);
+  const uint32_t p0 = blockIdx.x * 1024u + threadIdx.x;
+  uint32_t wv[4];
+  f16 sv[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    f16x2 p[4];
-    decode_word(wv[j], p);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) p[e] = p[e] * sc;
-    if (kMfma) {          // v3 words decode in k order: (k0,k1), (k2,k3), (k4,k5), (k6,k7)
-      o[j] = u32x4{as_u32(p[0]), as_u32(p[1]), as_u32(p[2]), as_u32(p[3])};
-    } else {              // canonical words decode to (k0,k4), (k1,k5), (k2,k6), (k3,k7)
-      const f16x2 a = {p[0][0], p[1][0]}, bb = {p[2][0], p[3][0]}, c = {p[0][1], p[1][1]}, d = {p[2][1], p[3][1]};
-      o[j] = u32x4{as_u32(a), as_u32(bb), as_u32(c), as_u32(d)};
+    const uint32_t p = p0 + 256u * j;
+    wv[j] = 0;
+    sv[j] = (f16)0.0f;
+    if (p < total) {
+      const uint32_t n = p / per_row, kp = p - n * per_row;        // output k = 8 kp .. 8 kp + 7
+      // MFMA layout: 16-byte piece (n, chunk kp / 16, quarter (kp / 4) % 4), word kp % 4 holds k in order
+      const size_t src = kMfma ? mfma_offset((int)n, (int)(kp >> 4), (int)((kp >> 2) & 3), N, K) + 4 * (kp & 3)
+                               : (size_t)p * 4;
+      wv[j] = *reinterpret_cast<const uint32_t*>(w + src);
+      sv[j] = s[(size_t)n * groups + (8 * kp) / (uint32_t)G];
     }
   }
-  u32x4* dst = reinterpret_cast<u32x4*>(out + (size_t)n * K + 32 * b);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) dst[j] = o[j];
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t p = p0 + 256u * j;
+    if (p >= total) continue;
+    const f16x2 sc = {sv[j], sv[j]};
+    f16x2 q[4];
+    decode_word(wv[j], q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = q[e] * sc;
+    u32x4 o;
+    if (kMfma) {          // v3 words decode in k order: (k0,k1), (k2,k3), (k4,k5), (k6,k7)
+      o = u32x4{as_u32(q[0]), as_u32(q[1]), as_u32(q[2]), as_u32(q[3])};
+    } else {              // canonical words decode to (k0,k4), (k1,k5), (k2,k6), (k3,k7)
+      const f16x2 a = {q[0][0], q[1][0]}, b = {q[2][0], q[3][0]}, c = {q[0][1], q[1][1]}, d = {q[2][1], q[3][1]};
+      o = u32x4{as_u32(a), as_u32(b), as_u32(c), as_u32(d)};
+    }
+    *reinterpret_cast<u32x4*>(out + (size_t)p * 8) = o;
+  }
 }
 
 template <bool kMfma>
@@ -71,8 +87,9 @@ __global__ __launch_bounds__(256) void relayout_kernel(const uint8_t* __restrict
 }
 
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st) {
-  const size_t total = (size_t)N * (K / 32);
-  dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  const size_t total = (size_t)N * (K / 8);
+  if (total >= (1ull << 32) - 1024) return hipErrorInvalidValue;      // piece indices are 32-bit
+  dim3 grid((unsigned)((total + 1023) / 1024)), block(256);
   if (mfma) return launch(dequant_kernel<true>, grid, block, 0, st, w, s, out, N, K, G);
   return launch(dequant_kernel<false>, grid, block, 0, st, w, s, out, N, K, G);
 }

@@ -37,6 +37,17 @@ struct GemvPlan {
   int S = 1;        // workgroups splitting K per row group (MFMA GEMM)
 };
 
+// launch shape of the prefill GEMM (M > 64)
+struct PrefillPlan {
+  int MT = 8;       // 16-row activation tiles per workgroup
+  int D = 2;        // weight chunks in flight per wave
+  int S = 1;        // workgroups splitting K per tile
+  int MG = 1;       // activation-row groups
+  int items = 1;    // workgroups: tiles x S
+  int NW = 4;       // waves per workgroup, 64 weight rows each
+  int XL = 1;       // chunks of x in flight
+};
+
 // process-wide launch-shape override for tuning sweeps (lowbit_set_launch_override); 0 = automatic
 struct GemvOverride {
   int waves = 0;
@@ -57,6 +68,8 @@ constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many byte
 // counters (zero before first use, left zero by every launch), followed by the fp32 partial sums [splits][M][N].
 constexpr int kGemmMaxGroups = 320;
 constexpr int kGemmTargetWaves = 1792;
+// prefill GEMM: K is split while the work items fill fewer than two rounds of this many workgroups
+constexpr int kPrefillTargetGroups = 256;
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
 // (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
@@ -84,6 +97,13 @@ int pick_rows_rowmajor(int N, int M);
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave);
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3);
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes);
+// prefill variants that compile without register spills (hipcc -O3, gfx950): an 8-wave workgroup has 256 registers
+// per wave, enough for 4 activation tiles and a 2-deep weight ring only
+constexpr bool prefill_fits(int MT, int D, int NW, int XL) {
+  return (D == 2 || XL == 1) && (NW == 4 || (MT == 4 && D == 2));
+}
+PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes);
+hipError_t gemm_prefill_launch(const GemvArgs& a, void* workspace, size_t workspace_bytes);
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st);
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
                           f16* v_cache, int M, int Hq, int Hkv, int L, hipStream_t st);

@@ -32,6 +32,8 @@ SIGNATURES = {
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_linear_fused": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_float, _vp,
                                 ctypes.c_size_t, _vp], _int),
+    "lowbit_w4_gemm_prefill": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp],
+                               _int),
     "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp], _int),
@@ -106,17 +108,19 @@ def _stream(device):
 
 WORKSPACE_COUNTER_BYTES = 16384
 WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (16 << 20)     # LOWBIT_WORKSPACE_BYTES
+PREFILL_WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (64 << 20)
 _WORKSPACES = {}
 
 
-def workspace(device, stream):
-    """The MFMA GEMM's workspace for (device, stream): zeroed once, kept for the life of the process (a graph captured
-    on the stream keeps using it), so calls on one stream never race on it and never reallocate it."""
+def workspace(device, stream, nbytes=WORKSPACE_BYTES):
+    """A GEMM workspace of `nbytes` for (device, stream): zeroed once, kept for the life of the process (a graph
+    captured on the stream keeps using it), so calls on one stream never race on it and never reallocate it. The
+    skinny GEMM and the prefill GEMM each have their own (WORKSPACE_BYTES, PREFILL_WORKSPACE_BYTES)."""
     import torch
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes)
     ws = _WORKSPACES.get(key)
     if ws is None:
-        ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
 
@@ -245,6 +249,26 @@ class NativeExt:
             check(self.lib.lowbit_w4_linear_fused(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group,
                                                   int(epilogue), ptr(aux) if aux is not None else None,
                                                   ptr(nw) if nw is not None else None, float(eps), ptr(ws),
+                                                  ws.numel(), st))
+        return y
+
+    def w4_gemm_prefill(self, x, w, s, group, epilogue=EPI_STORE, aux=None, out=None):
+        """x [M, K] (any M, meant for M > 64) times the MFMA-layout weight, int4 read directly, with the epilogue
+        fused into the store; returns y ([M, N], or [M, N / 2] for EPI_SILU_MUL)."""
+        import torch
+        _check_tensors(x, w, s, group)
+        m, n = x.shape[0], w.shape[0]
+        cols = n // 2 if epilogue == EPI_SILU_MUL else n
+        y = out if out is not None else torch.empty((m, cols), dtype=torch.float16, device=x.device)
+        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous():
+            raise RuntimeError("out must be a contiguous float16 [M, N] (or [M, N/2] for silu-mul) tensor")
+        if aux is not None and (aux.dtype != torch.float16 or not aux.is_contiguous() or aux.device != x.device):
+            raise RuntimeError("aux must be a contiguous float16 tensor on the same GPU")
+        with _DeviceGuard(x.device):
+            st = _stream(x.device)
+            ws = workspace(x.device, st, PREFILL_WORKSPACE_BYTES)
+            check(self.lib.lowbit_w4_gemm_prefill(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group,
+                                                  int(epilogue), ptr(aux) if aux is not None else None, ptr(ws),
                                                   ws.numel(), st))
         return y
 

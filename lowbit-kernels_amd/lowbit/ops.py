@@ -156,6 +156,11 @@ def dequant(wq, layout=None):
 # at M = 1; from M = 2 to 64 the MFMA kernel beats dequantize + hipBLASLt 2-6x and fp16 hipBLASLt on every shape, so
 # the width split of the reference's rule (which came from a T4) no longer matters.
 AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 64, 64, 3072
+# Beyond the MFMA kernel's rows (prefill), a weight on the mma layout with K >= AUTO_PREFILL_MIN_K goes to the
+# int4-direct prefill GEMM (prefill()), everything else to dequantize + BLAS. From the MI355X sweep at M = 128, 512,
+# 2048 on the Qwen2.5-3B / 7B projections: dequantize (4.4-4.8 TB/s) + hipBLASLt wins at K = 2048, 3584 and 11008;
+# the int4 kernel wins only on the long-K 7B down projection (K = 18944: 1.06x, 1.56x, 1.13x).
+AUTO_PREFILL_MIN_K = 16384
 
 
 def gemm_chunked(x, wq, chunk=64):
@@ -175,10 +180,23 @@ def auto_version(m, wq):
     return None
 
 
+def prefill(x, wq):
+    """x [M, K] times an mma-layout weight with the int4-direct prefill GEMM (any M; fp32 accumulation of exactly the
+    dequantized fp16 weights, as dequantize + BLAS computes)."""
+    if wq.packed_mma is None:
+        raise ValueError("the prefill GEMM reads packed_mma, which this W4Weight does not keep")
+    return ext().w4_gemm_prefill(x.contiguous(), wq.packed_mma, wq.scales, wq.group)
+
+
+def prefill_path(m, wq):
+    """True when linear() sends m rows to the int4 prefill GEMM rather than dequantize + BLAS (auto routing only)."""
+    return auto_version(m, wq) is None and wq.packed_mma is not None and wq.k >= AUTO_PREFILL_MIN_K
+
+
 def linear(x, wq, max_gemv_rows=8, version=0):
     """Decode (few rows): an INT4 kernel (v6 GEMV for one row, v5 MFMA beyond). Prefill (many rows): dequantize, then
-    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm). version 0 = auto_version; a fixed version runs up to
-    min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above that."""
+    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or on long K the int4 prefill GEMM (prefill_path). version 0 =
+    auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above."""
     m = x.shape[0]
     if m == 0:
         return x.new_empty(0, wq.n)
@@ -190,4 +208,6 @@ def linear(x, wq, max_gemv_rows=8, version=0):
         raise ValueError(f"version must be 0 (auto) or one of {sorted(MAX_ROWS)}")
     if v is not None:
         return gemv(x, wq, v)
+    if version == 0 and prefill_path(m, wq):
+        return prefill(x, wq)
     return torch.nn.functional.linear(x, dequant(wq, "mma" if wq.packed_mma is not None else "canonical"))

@@ -19,6 +19,7 @@ def calls(monkeypatch):
     seen = []
     monkeypatch.setattr(ops, "gemv", lambda x, wq, v, rpw=0: seen.append(v) or torch.zeros(x.shape[0], wq.n))
     monkeypatch.setattr(ops, "dequant", lambda wq, layout=None: seen.append("dequant") or torch.zeros(wq.n, wq.k))
+    monkeypatch.setattr(ops, "prefill", lambda x, wq: seen.append("prefill") or torch.zeros(x.shape[0], wq.n))
     return seen
 
 
@@ -44,6 +45,19 @@ def test_reference_table_with_the_t4_constants(calls, monkeypatch):
         calls.clear()
         ops.linear(torch.zeros(m, 256), weight(n))
         assert calls == [want]
+
+
+def test_prefill_rule(calls):
+    """Beyond the MFMA kernel's rows, long-K weights on the mma layout take the int4 prefill GEMM; short K, other
+    layouts and fixed versions keep dequantize + BLAS; decode rows never reach it."""
+    kmin, rows = ops.AUTO_PREFILL_MIN_K, ops.AUTO_V5_ROWS + 1
+    for m, k, layouts, version, want in [(rows, kmin, ("mma",), 0, "prefill"), (512, 2 * kmin, ("mma",), 0, "prefill"),
+                                         (rows, kmin - 128, ("mma",), 0, "dequant"), (rows, kmin, ("canonical",), 0, "dequant"),
+                                         (rows, kmin, ("mma",), 5, "dequant"), (1, kmin, ("mma",), 0, 6),
+                                         (rows - 1, kmin, ("mma",), 0, 5)]:
+        calls.clear()
+        ops.linear(torch.zeros(m, k), weight(1024, k, layouts), version=version)
+        assert calls == [want], (m, k, layouts, version)
 
 
 @pytest.mark.parametrize("layouts,m,want", [(("canonical", "v3"), 1, 4), (("canonical", "v3"), 8, 4),
