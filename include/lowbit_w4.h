@@ -143,9 +143,14 @@ int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_f
 
 /* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]
  * (at most L); scores scaled by `scale`, softmax and P.V in fp32. max_keys: an upper bound on positions[m] + 1 over
- * the calls that will run (sizes the launch; a captured graph keeps it). Hq / Hkv in {1, 2, 4, 6, 7, 8}. */
+ * the calls that will run (sizes the launch; a captured graph keeps it; keys past it are still attended, by the last
+ * key partition). Hq / Hkv in {1, 2, 4, 6, 7, 8}. workspace (optional, 16-byte aligned, no initial contents needed):
+ * when there are too few (token, head group) blocks to fill the GPU and max_keys >= 512, the keys are split into
+ * partitions whose fp32 partial softmax sums (blocks x partitions x (2 + 128) x 4 bytes, at most workspace_bytes) a
+ * second launch combines in partition order (same bits on every call for a given launch); NULL = no split. */
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
-                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* stream);
+                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 /* ---- HBM bandwidth probes (the measured peak that kernel bandwidths are quoted against) ----
  * The reference measures its peak with a torch device copy and a torch sum over 256 MiB (bench/gpu_run.py:133-141);

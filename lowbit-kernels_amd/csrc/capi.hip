@@ -293,7 +293,8 @@ int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_f
 }
 
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
-                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* stream) {
+                     int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream) {
   if (!q || !k_cache || !v_cache || !positions || !out) return fail(LOWBIT_ERR_ARG, "null pointer argument");
   if (M < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || !fits_int(M * Hkv) || !fits_int(L * 128 * Hkv))
     return fail(LOWBIT_ERR_SHAPE, "attention: M, Hq, Hkv (dividing Hq), L must be positive");
@@ -301,11 +302,12 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
   if (!(g == 1 || g == 2 || g == 4 || g == 6 || g == 7 || g == 8))
     return fail(LOWBIT_ERR_SHAPE, "attention takes 1, 2, 4, 6, 7 or 8 query heads per KV head");
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return fail(LOWBIT_ERR_ALIGN, "attention needs 16-byte aligned q and caches");
+  if (workspace && !aligned16(workspace)) return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned");
   if (int rc = check_device()) return rc;
   return hip_status(attention_launch(static_cast<const f16*>(q), static_cast<const f16*>(k_cache),
                                      static_cast<const f16*>(v_cache), positions, static_cast<f16*>(out), (int)M,
                                      (int)Hq, (int)Hkv, (int)L, (int)std::max<int64_t>(1, std::min(max_keys, L)), scale,
-                                     static_cast<hipStream_t>(stream)),
+                                     workspace, workspace ? workspace_bytes : 0, static_cast<hipStream_t>(stream)),
                     "attention");
 }
 

@@ -3,6 +3,8 @@
 // causal GQA attention over the cache. Each follows the arithmetic of the module it replaces (transformers
 // Qwen2RMSNorm, apply_rotary_pos_emb + StaticCache.update, scaled_dot_product_attention with a causal mask), with
 // the same fp16 roundings where the torch ops round.
+#include <algorithm>
+
 #include "kernels.hpp"
 
 namespace lowbit {
@@ -95,18 +97,25 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
 // reads four whole cache rows, the lane's slice of q stays in registers, a score is a 16-lane DPP sum, and the
 // probabilities never leave the lane that multiplies them into V. Waves take blocks of KB keys; the row groups and
 // the waves are merged at the end (lane shuffles, then LDS).
+// When (token, group) blocks alone cannot fill the chip (a decode step), the keys are also split into P partitions
+// of CH keys (grid.y): each block writes its partial (max, sum, unnormalized output) to the workspace and
+// attention_combine, launched next on the stream, merges the P partials in partition order. The kernel boundary makes
+// the partials visible across XCDs; an in-kernel last-arrival merge would need an agent-scope release per block
+// (an L2 write-back, serialized per XCD), which measured slower than the second launch.
 template <int G, int KB>
 __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k_cache, const f16* __restrict__ v_cache,
-    const int64_t* __restrict__ pos, f16* __restrict__ out, int Hq, int Hkv, int L, float scale) {
+    const int64_t* __restrict__ pos, f16* __restrict__ out, int Hq, int Hkv, int L, float scale, int CH,
+    float* __restrict__ part) {
   constexpr int NI = KB / 4;                                 // 16-byte loads per lane and step, per K and per V
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int groups = Hq / G;
+  const int groups = Hq / G, P = gridDim.y, pid = blockIdx.y;
   const int m = blockIdx.x / groups, h0 = (blockIdx.x % groups) * G, hk = h0 / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
   const int rg = lane >> 4, dl = (lane & 15) * 8;          // key row-group, first dim of the lane's slice
   const int64_t pm = pos[m];
   const int nkeys = (int)min((int64_t)L, pm + 1), last = nkeys - 1;
+  const int kbeg = pid * CH, kend = pid == P - 1 ? nkeys : min(nkeys, kbeg + CH);   // this block's keys
   u32x4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const u32x4*>(q + ((size_t)m * Hq + h0 + g) * kHeadDim + dl);
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[g][d] = 0.f;
   }
-  for (int base = wave * KB; base < nkeys; base += KB * W) {
+  for (int base = kbeg + wave * KB; base < kend; base += KB * W) {
     // step keys base + 4 i + rg, i < NI (rows past the end are clamped and masked)
     u32x4 kq[NI], vq[NI];
 #pragma unroll
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
 #pragma unroll
         for (int e = 0; e < 4; ++e) a = dot2(as_f16x2(qv[g][e]), as_f16x2(kq[i][e]), a);
         a = row_sum(a) * scale;                              // the key's score, in all 16 lanes of the row group
-        s[i] = base + 4 * i + rg <= last ? a : -INFINITY;
+        s[i] = base + 4 * i + rg < kend ? a : -INFINITY;
         bm = fmaxf(bm, s[i]);
       }
       bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
@@ -185,6 +194,8 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
     }
   }
   __syncthreads();
+  // partial of this block: [G][2 + D] floats (max, sum, then the unnormalized output), per (token, group, partition)
+  float* mine = part + (((size_t)blockIdx.x * P + pid) * G) * (2 + kHeadDim);
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
     const int g = idx / kHeadDim, d = idx % kHeadDim;
     float gm = -INFINITY;
@@ -197,8 +208,49 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
       num = fmaf(f, os[(w * G + g) * kHeadDim + d], num);
       den = fmaf(f, st[(w * G + g) * 2 + 1], den);
     }
-    out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
+    if (P == 1) {
+      out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
+    } else {
+      mine[g * (2 + kHeadDim) + 2 + d] = num;
+      if (d == 0) {
+        mine[g * (2 + kHeadDim)] = gm;
+        mine[g * (2 + kHeadDim) + 1] = den;
+      }
+    }
   }
+}
+
+// out[m][h][d] from the P <= kAttnMaxParts partials of attention_kernel: max over partitions, then the rescaled sums,
+// in partition order (partitions that saw no key hold max = -inf and are skipped; partition 0 always holds key 0).
+// The loops run to the compile-time bound, so all of a thread's loads are requested before the first is used.
+__global__ __launch_bounds__(256) void attention_combine(const float* __restrict__ part, f16* __restrict__ out,
+                                                         int blocks, int G, int P, int Hq) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= blocks * G * kHeadDim) return;
+  const int b = idx / (G * kHeadDim), g = (idx / kHeadDim) % G, d = idx % kHeadDim;
+  const int groups = Hq / G, m = b / groups, h = (b % groups) * G + g;
+  const float* all = part + (size_t)b * P * G * (2 + kHeadDim) + (size_t)g * (2 + kHeadDim);
+  const size_t stride = (size_t)G * (2 + kHeadDim);
+  float pm[kAttnMaxParts], ps[kAttnMaxParts], po[kAttnMaxParts];
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) {
+    const bool live = p < P;
+    pm[p] = live ? all[p * stride] : -INFINITY;
+    ps[p] = live ? all[p * stride + 1] : 0.f;
+    po[p] = live ? all[p * stride + 2 + d] : 0.f;
+  }
+  float gm = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) gm = fmaxf(gm, pm[p]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) {
+    if (pm[p] == -INFINITY) continue;
+    const float f = expf(pm[p] - gm);
+    num = fmaf(f, po[p], num);
+    den = fmaf(f, ps[p], den);
+  }
+  out[((size_t)m * Hq + h) * kHeadDim + d] = (f16)(num / den);
 }
 
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st) {
@@ -215,27 +267,44 @@ hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_f
 namespace {
 template <int G, int KB>
 hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
-                            int Hkv, int L, int max_keys, float scale, hipStream_t st) {
+                            int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
   const int max_waves = (G == 1 && KB == 32) ? 16 : 8;
+  const long blocks = (long)M * (Hq / G);
+  // key partitions: when the (token, group) blocks cannot fill the chip, split the keys so that about
+  // kAttnTargetBlocks blocks run, each with at least kAttnMinKeys keys, within the workspace and its counters
+  int P = 1;
+  if (ws && blocks < kAttnTargetBlocks && max_keys >= kAttnMinSplitKeys) {
+    P = (int)std::min<long>({(kAttnTargetBlocks + blocks - 1) / blocks, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
+                             (long)kAttnMaxParts});
+    const size_t per = (size_t)blocks * G * (2 + kHeadDim) * sizeof(float);
+    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, ws_bytes / per));
+  }
+  const int CH = ((max_keys + P - 1) / P + KB - 1) / KB * KB;   // keys per partition, whole steps
+  P = (max_keys + CH - 1) / CH;
   int waves = 1;                                              // enough waves to give each one step of keys
-  while (waves < max_waves && waves * KB < max_keys) waves *= 2;
+  while (waves < max_waves && waves * KB < CH) waves *= 2;
   const size_t lds = (size_t)waves * G * 2 * 4 + (size_t)waves * G * kHeadDim * 4;
-  return launch(attention_kernel<G, KB>, dim3(M * (Hq / G)), dim3(64 * waves), lds, st, q, k, v, pos, out, Hq, Hkv,
-                L, scale);
+  float* part = static_cast<float*>(ws);
+  hipError_t e = launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos,
+                        out, Hq, Hkv, L, scale, CH, part);
+  if (e != hipSuccess || P == 1) return e;
+  const long threads = blocks * G * kHeadDim;
+  return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, (int)blocks,
+                G, P, Hq);
 }
 }  // namespace
 
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
-                            int Hkv, int L, int max_keys, float scale, hipStream_t st) {
+                            int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
   if ((long)M * Hkv < 64)                                     // few tokens: one query head per block, short steps
-    return launch_attention<1, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    return launch_attention<1, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
   switch (Hq / Hkv) {
-    case 1: return launch_attention<1, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 2: return launch_attention<2, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 4: return launch_attention<4, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 6: return launch_attention<6, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 7: return launch_attention<7, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
-    case 8: return launch_attention<8, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, st);
+    case 1: return launch_attention<1, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
+    case 2: return launch_attention<2, 64>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
+    case 4: return launch_attention<4, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
+    case 6: return launch_attention<6, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
+    case 7: return launch_attention<7, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
+    case 8: return launch_attention<8, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
     default: return hipErrorInvalidValue;
   }
 }

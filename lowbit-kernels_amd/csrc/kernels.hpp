@@ -70,6 +70,12 @@ constexpr int kGemmMaxGroups = 320;
 constexpr int kGemmTargetWaves = 1792;
 // prefill GEMM: K is split while the work items fill fewer than two rounds of this many workgroups
 constexpr int kPrefillTargetGroups = 256;
+// decode attention: when the cache holds at least kAttnMinSplitKeys keys, keys are split across blocks while
+// (token, head group) blocks number fewer than kAttnTargetBlocks, down to kAttnMinKeys keys per block
+constexpr int kAttnTargetBlocks = 256;
+constexpr int kAttnMinKeys = 64;
+constexpr int kAttnMinSplitKeys = 512;
+constexpr int kAttnMaxParts = 16;
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
 // (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
@@ -110,7 +116,7 @@ hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_f
 hipError_t hbm_read_launch(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t stream);
 hipError_t hbm_copy_launch(const void* src, void* dst, size_t bytes, int blocks, hipStream_t stream);
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
-                            int Hkv, int L, int max_keys, float scale, hipStream_t st);
+                            int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st);
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st);
 hipError_t relayout_launch(const uint8_t* src, uint8_t* dst, int N, int K, bool mfma, hipStream_t st);
 hipError_t quantize_launch(const void* w, int dtype, uint8_t* packed, f16* scales, int N, int K, int G,

@@ -36,7 +36,8 @@ SIGNATURES = {
                                _int),
     "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
-    "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp], _int),
+    "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
+                          _vp], _int),
     "lowbit_hbm_read": ([_vp, _i64, _vp, _i64, _vp], _int),
     "lowbit_hbm_copy": ([_vp, _vp, _i64, _i64, _vp], _int),
     "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
@@ -109,6 +110,7 @@ def _stream(device):
 WORKSPACE_COUNTER_BYTES = 16384
 WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (16 << 20)     # LOWBIT_WORKSPACE_BYTES
 PREFILL_WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (64 << 20)
+ATTENTION_WORKSPACE_BYTES = 4 << 20
 _WORKSPACES = {}
 
 
@@ -285,11 +287,15 @@ class NativeExt:
             check(self.lib.lowbit_rope_kv(ptr(qkv), ptr(positions), ptr(inv_freq), ptr(q_out), ptr(k_cache),
                                           ptr(v_cache), qkv.shape[0], hq, hkv, k_cache.shape[1], _stream(qkv.device)))
 
-    def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale):
+    def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale, split=True):
+        """split=False runs one block per (token, head group), without the key partitions and their workspace."""
         with _DeviceGuard(q.device):
+            st = _stream(q.device)
+            ws = workspace(q.device, st, ATTENTION_WORKSPACE_BYTES) if split else None
             check(self.lib.lowbit_attention(ptr(q), ptr(k_cache), ptr(v_cache), ptr(positions), ptr(out), q.shape[0],
                                             hq, hkv, k_cache.shape[1], int(max_keys), float(scale),
-                                            _stream(q.device)))
+                                            ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0,
+                                            st))
 
     # ---- bandwidth probes (lowbit_hbm_read, lowbit_hbm_copy) ----
     def hbm_read(self, buf, sink, blocks):

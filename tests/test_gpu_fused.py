@@ -103,7 +103,9 @@ def test_rope_and_cache_write_match_transformers(cuda):
 
 
 @pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
-                                                (28, 4, 300, list(range(200, 248))), (2, 1, 64, [10, 40])])
+                                                (28, 4, 300, list(range(200, 248))), (2, 1, 64, [10, 40]),
+                                                (16, 2, 4096, [4095]), (28, 4, 2048, [5, 2047]),
+                                                (16, 2, 768, list(range(512, 528)))])
 def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
     g = torch.Generator(device="cuda").manual_seed(hq + L)
     m = len(positions)
@@ -111,9 +113,7 @@ def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
     k_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
     v_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
     pos = torch.tensor(positions, device="cuda")
-    out = torch.empty(m, hq * 128, dtype=torch.half, device="cuda")
     scale = 1 / math.sqrt(128)
-    ops.ext().attention(q, k_cache, v_cache, pos, out, hq, hkv, L, scale)
     grp = hq // hkv
     ref = torch.empty(m, hq, 128, dtype=torch.float32, device="cuda")
     for i, p in enumerate(positions):
@@ -121,7 +121,15 @@ def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
             kk, vv = k_cache[h // grp, :p + 1].float(), v_cache[h // grp, :p + 1].float()
             w = torch.softmax(kk @ q[i, h].float() * scale, 0)
             ref[i, h] = w @ vv
-    assert rel(out.view(m, hq, 128), ref.double()) < 3e-3
+    # one block per (token, head group), and with the keys split into partitions (decode shapes); a max_keys below
+    # the real key count still attends every key (the last partition takes the rest)
+    for split, max_keys in ((False, L), (True, L), (True, 40)):
+        out = torch.empty(m, hq * 128, dtype=torch.half, device="cuda")
+        ops.ext().attention(q, k_cache, v_cache, pos, out, hq, hkv, max_keys, scale, split=split)
+        assert rel(out.view(m, hq, 128), ref.double()) < 3e-3, (split, max_keys)
+        again = torch.empty_like(out)
+        ops.ext().attention(q, k_cache, v_cache, pos, again, hq, hkv, max_keys, scale, split=split)
+        assert torch.equal(out, again), (split, max_keys)
 
 
 @pytest.fixture(scope="module")
