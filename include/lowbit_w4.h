@@ -152,6 +152,12 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* fp16 GEMV for the tied fp16 lm_head of a decode step (or the last row of a prefill): y [M, N] = fp16(x [M, K] . W^T)
+ * with W fp16 [N, K] row-major, fp32 accumulation, 1 <= M <= 4, K % 8 == 0, M * K * 2 <= 65536, x and W 16-byte
+ * aligned. No counterpart in the reference (its head is torch.nn.functional.linear, cuBLAS); it replaces that call
+ * in the fused decoder, where hipBLASLt streams the 622 MB Qwen2.5-3B head at ~3 TB/s. */
+int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* ---- HBM bandwidth probes (the measured peak that kernel bandwidths are quoted against) ----
  * The reference measures its peak with a torch device copy and a torch sum over 256 MiB (bench/gpu_run.py:133-141);
  * these are streaming kernels of this library for the same two figures. hbm_read reads `bytes` (a multiple of 16,

@@ -253,6 +253,71 @@ __global__ __launch_bounds__(256) void attention_combine(const float* __restrict
   out[((size_t)m * Hq + h) * kHeadDim + d] = (f16)(num / den);
 }
 
+// fp16 GEMV for the (tied) lm_head, M <= 4: y[m][n] = fp16(sum_k x[m][k] W[n][k]), W fp16 [N][K] row-major, fp32
+// accumulation. A bandwidth kernel: the workgroup stages x[M][K] in LDS once (one barrier), then each wave streams
+// RW weight rows with 16-byte non-temporal loads (lane l takes k = 512 c + 8 l .. + 7 of chunk c, so every load is
+// one contiguous 1 KB), two chunks of every row in flight, dot2 against x from LDS, and a wave reduction per row.
+template <int M, int RW>
+__global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                                       f16* __restrict__ y, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kp = K >> 3;                                     // 16-byte pieces per row
+  for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
+  __syncthreads();
+  const int n0 = (blockIdx.x * 4 + wave) * RW;
+  if (n0 >= N) return;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)n0 * K, (uint32_t)(min(RW, N - n0) * K * 2));
+  float acc[RW][M];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
+  const int nc = (kp + 63) >> 6;                             // 512-k chunks
+  for (int c0 = 0; c0 < nc; c0 += 2) {
+    u32x4 wv[2][RW];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = 64 * (c0 + u) + lane;                    // this lane's piece of the chunk
+#pragma unroll
+      for (int r = 0; r < RW; ++r) wv[u][r] = buffer_load16_nt(wr, p < kp ? 2 * (r * K + 8 * p) : kOutOfRange);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = 64 * (c0 + u) + lane;
+      if (p >= kp) break;
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const u32x4 xv = xs[m * kp + p];
+#pragma unroll
+        for (int r = 0; r < RW; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][m] = dot2(as_f16x2(wv[u][r][e]), as_f16x2(xv[e]), acc[r][m]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float v = wave_sum(acc[r][m]);
+      if (lane == 0 && n0 + r < N) y[(size_t)m * N + n0 + r] = (f16)v;
+    }
+}
+
+hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st) {
+  constexpr int RW = 8;
+  const dim3 grid((unsigned)((N + 4 * RW - 1) / (4 * RW))), block(256);
+  const size_t lds = (size_t)M * K * 2;
+  switch (M) {
+    case 1: return launch(gemv_f16_kernel<1, RW>, grid, block, lds, st, x, w, y, N, K);
+    case 2: return launch(gemv_f16_kernel<2, RW>, grid, block, lds, st, x, w, y, N, K);
+    case 3: return launch(gemv_f16_kernel<3, RW>, grid, block, lds, st, x, w, y, N, K);
+    default: return launch(gemv_f16_kernel<4, RW>, grid, block, lds, st, x, w, y, N, K);
+  }
+}
+
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st) {
   return launch(rmsnorm_kernel, dim3(M), dim3(256), 0, st, x, w, out, H, eps);
 }

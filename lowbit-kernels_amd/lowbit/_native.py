@@ -38,6 +38,7 @@ SIGNATURES = {
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
+    "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
     "lowbit_hbm_read": ([_vp, _i64, _vp, _i64, _vp], _int),
     "lowbit_hbm_copy": ([_vp, _vp, _i64, _i64, _vp], _int),
     "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
@@ -296,6 +297,21 @@ class NativeExt:
                                             hq, hkv, k_cache.shape[1], int(max_keys), float(scale),
                                             ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0,
                                             st))
+
+    def f16_gemv(self, x, w, out=None):
+        """fp16 x [M <= 4, K] times fp16 W [N, K]^T -> fp16 [M, N] (fp32 accumulation)."""
+        import torch
+        if not (x.is_cuda and w.is_cuda and x.device == w.device):
+            raise RuntimeError("x and w must be on the same GPU")
+        if x.dtype != torch.float16 or w.dtype != torch.float16 or not (x.is_contiguous() and w.is_contiguous()):
+            raise RuntimeError("x and w must be contiguous float16")
+        if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
+            raise RuntimeError("x [M, K] and w [N, K]")
+        y = out if out is not None else torch.empty((x.shape[0], w.shape[0]), dtype=torch.float16, device=x.device)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_f16_gemv(ptr(x), ptr(w), ptr(y), x.shape[0], w.shape[0], x.shape[1],
+                                           _stream(x.device)))
+        return y
 
     # ---- bandwidth probes (lowbit_hbm_read, lowbit_hbm_copy) ----
     def hbm_read(self, buf, sink, blocks):

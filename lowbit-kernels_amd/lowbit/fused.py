@@ -127,9 +127,17 @@ class FusedQwen2:
         self.k_cache.zero_()
         self.v_cache.zero_()
 
+    def logits(self, xn):
+        """The tied fp16 head: the library's fp16 GEMV for up to 4 rows (a bandwidth kernel; hipBLASLt streams the
+        head at ~3 TB/s at these shapes), hipBLASLt beyond."""
+        if xn.shape[0] <= 4 and xn.shape[1] * xn.shape[0] * 2 <= 65536:
+            return ops.ext().f16_gemv(xn, self.head)
+        return F.linear(xn, self.head)
+
     @torch.inference_mode()
-    def forward(self, tokens, positions):
-        """tokens, positions: int64 [M] on the GPU -> logits fp16 [M, vocab]."""
+    def forward(self, tokens, positions, last_only=False):
+        """tokens, positions: int64 [M] on the GPU -> logits fp16 [M, vocab] ([1, vocab] for the last position only
+        when last_only, as a prefill needs)."""
         ext = ops.ext()
         m = tokens.shape[0]
         h = F.embedding(tokens, self.embed)
@@ -153,8 +161,10 @@ class FusedQwen2:
                 ext.rmsnorm(h, lay["post_norm"], self.eps, out=xn)
                 act = lay["gu"](xn, EPI_SILU_MUL)
             lay["down"](act, EPI_RESIDUAL, h, out=h)
+        if last_only:
+            h, xn = h[-1:], xn[-1:]
         ext.rmsnorm(h, self.final_norm, self.eps, out=xn)
-        return F.linear(xn, self.head)
+        return self.logits(xn)
 
     __call__ = forward
 
@@ -177,7 +187,7 @@ class FusedDecoder:
         if p > self.f.max_len:
             raise ValueError(f"a {p}-token prompt does not fit a {self.f.max_len}-token cache")
         self.f.reset()
-        logits = self.f(ids.view(-1), torch.arange(p, device=ids.device))
+        logits = self.f(ids.view(-1), torch.arange(p, device=ids.device), last_only=True)
         self.pos = p
         return logits[-1]
 

@@ -58,6 +58,10 @@ def _msg(rc):
     (lambda l: l.lowbit_set_launch_override(3, 0, 0), 8, "waves_per_group"),
     (lambda l: l.lowbit_set_launch_override(4, 5, 0), 8, "ring"),
     (lambda l: l.lowbit_set_launch_override(4, 4, 33), 8, "k_splits"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 5, 16, 128, None), 5, "1..4 rows"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 1, 16, 12, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 4, 16, 16384, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv(ctypes.c_void_p(4100), FAKE, FAKE, 1, 16, 128, None), 4, "16-byte"),
     (lambda l: l.lowbit_hbm_read(None, 1024, FAKE, 256, None), 1, "null pointer"),
     (lambda l: l.lowbit_hbm_read(FAKE, 1000, FAKE, 256, None), 3, "multiple of 16"),
     (lambda l: l.lowbit_hbm_read(FAKE, 1024, FAKE, 0, None), 3, "blocks"),

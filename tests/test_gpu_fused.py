@@ -66,6 +66,25 @@ def test_fused_input_norm_matches_norm_then_projection(cuda, k, n):
         ext.w4_linear_fused(x2, wq.packed_mma, wq.scales, wq.group, fused.EPI_STORE, norm=(nw, 1e-6))
 
 
+@pytest.mark.parametrize("n,k", [(1000, 2048), (4099, 1536), (64, 8), (151936, 2048), (7, 16384)])
+def test_f16_gemv_against_fp32(cuda, n, k):
+    """The fp16 head GEMV: the fp16 rounding of the exact product, up to fp32 summation noise (half an fp16 ulp plus
+    2^-16 of the output RMS)."""
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    for m in range(1, 5):
+        if m * k * 2 > 65536:
+            continue
+        x = torch.randn(m, k, generator=g, device="cuda").half()
+        y = ops.ext().f16_gemv(x, w)
+        ref = x.double() @ w.double().t()
+        err = (y.double() - ref).abs()
+        ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14))) - 10)
+        assert bool((err <= 0.5 * ulp + 2.0 ** -16 * ref.pow(2).mean().sqrt()).all()), (n, k, m)
+    with pytest.raises(RuntimeError, match="1..4 rows"):
+        ops.ext().f16_gemv(torch.zeros(5, k, dtype=torch.half, device="cuda"), w)
+
+
 def test_rmsnorm_matches_qwen2_rmsnorm(cuda):
     from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
     g = torch.Generator().manual_seed(1)
