@@ -137,9 +137,22 @@ int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int6
 
 /* RoPE (rotate-half, head_dim 128, angle = positions[m] * inv_freq[i] in fp32) on the q and k heads of a fused qkv
  * projection output [M][(Hq + 2 Hkv) * 128]; rotated q -> q_out [M][Hq][128]; rotated k and v -> k_cache, v_cache
- * [Hkv][L][128] at row positions[m] (device int64; rows outside 0..L-1 are not written). */
+ * [Hkv][L][128] at row positions[m] (device int64; rows outside 0..L-1 are not written). permuted != 0: qkv holds
+ * each head's 128 values in the RoPE-permuted order of lowbit_w4_qkv_rope (row 16 (d / 8) + d % 8 for dim d < 64,
+ * that row + 8 for dim d + 64). */
 int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
-                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, void* stream);
+                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int permuted, void* stream);
+
+/* One decode token's q|k|v projection with RoPE and the cache write fused into its store (no counterpart in the
+ * reference; it replaces lowbit_w4_linear_fused(LOWBIT_EPI_BIAS) followed by lowbit_rope_kv). The weight's rows are
+ * permuted per 128-row head so that 16-row tile j holds dims 8 j .. 8 j + 7 and 64 + 8 j .. 64 + 8 j + 7 (rope_kv's
+ * permuted layout); bias [N] in the same order. x [1, K]: the layer input, normalized first when norm_weight is given
+ * (RMSNorm, as lowbit_w4_linear_fused). q -> q_out [Hq][128]; k, v -> k_cache / v_cache [Hkv][L][128] at row
+ * positions[0] (device int64; outside 0..L-1 nothing is written). The same bits as the unfused pair. */
+int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, int64_t K, int64_t group,
+                       const void* bias, const void* norm_weight, float eps, const int64_t* positions,
+                       const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv,
+                       int64_t L, void* stream);
 
 /* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]
  * (at most L); scores scaled by `scale`, softmax and P.V in fp32. max_keys: an upper bound on positions[m] + 1 over

@@ -281,15 +281,39 @@ int lowbit_rmsnorm(const void* x, const void* weight, void* out, int64_t M, int6
 }
 
 int lowbit_rope_kv(const void* qkv, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
-                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, void* stream) {
+                   void* v_cache, int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int permuted, void* stream) {
   if (!qkv || !positions || !inv_freq || !q_out || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
   if (M < 1 || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || !fits_int(M * (Hq + 2 * Hkv) * 64) || !fits_int(L * 128 * Hkv))
     return fail(LOWBIT_ERR_SHAPE, "rope_kv: M, Hq, Hkv (dividing Hq), L must be positive");
   if (int rc = check_device()) return rc;
   return hip_status(rope_kv_launch(static_cast<const f16*>(qkv), positions, inv_freq, static_cast<f16*>(q_out),
                                    static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), (int)M, (int)Hq, (int)Hkv,
-                                   (int)L, static_cast<hipStream_t>(stream)),
+                                   (int)L, permuted != 0, static_cast<hipStream_t>(stream)),
                     "rope_kv");
+}
+
+int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, int64_t K, int64_t group,
+                       const void* bias, const void* norm_weight, float eps, const int64_t* positions,
+                       const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv,
+                       int64_t L, void* stream) {
+  if (int rc = check_common(x, w, s, q_out, 1, N, K, group)) return rc;
+  if (!bias || !positions || !inv_freq || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || N != (Hq + 2 * Hkv) * 128 || !fits_int(L * 128 * Hkv))
+    return fail(LOWBIT_ERR_SHAPE, "qkv_rope: N must be (Hq + 2 Hkv) * 128 with Hkv dividing Hq, L positive");
+  if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
+  if (int rc = check_mfma_layout_limits(N, K, group, true)) return rc;
+  if (norm_weight && (K > 16384 || !aligned16(norm_weight)))
+    return fail(LOWBIT_ERR_ARG, "the fused input norm takes K <= 16384 and a 16-byte aligned weight");
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(q_out),
+             1, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
+  a.epi.mode = kEpiRopeQKV;
+  a.epi.aux = static_cast<const f16*>(bias);
+  a.epi.rope = RopeArgs{positions, inv_freq, static_cast<f16*>(q_out), static_cast<f16*>(k_cache),
+                        static_cast<f16*>(v_cache), (int)Hq, (int)Hkv, (int)L};
+  a.norm_w = static_cast<const f16*>(norm_weight);
+  a.eps = eps;
+  return hip_status(gemv_mfma_layout_launch(a, 0), "w4_qkv_rope");
 }
 
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,

@@ -125,6 +125,21 @@ __device__ __forceinline__ f16 epi_value(int mode, const f16* __restrict__ aux, 
   return v;
 }
 
+// RoPE of one dim pair (d, d + 64) at position p as transformers computes it for fp16 models: angle =
+// fp32(p * inv_freq[d]), cos and sin in fp32 rounded to fp16, x * cos + rotate_half(x) * sin with each product and
+// the sum rounded to fp16 (no contraction)
+__device__ __forceinline__ void rope_pair(f16 x1, f16 x2, int64_t p, float inv_f, f16& o1, f16& o2) {
+#pragma clang fp contract(off)
+  const float ang = (float)p * inv_f;
+  const f16 c = (f16)cosf(ang), s = (f16)sinf(ang);
+  o1 = (f16)(x1 * c) + (f16)(-x2 * s);
+  o2 = (f16)(x2 * c) + (f16)(x1 * s);
+}
+
+// row of head dim d (< 64: the first of the pair) in the RoPE-permuted q|k|v layout: tile d / 8, rows 0..7 hold dims
+// 8 t .. 8 t + 7 and rows 8..15 their partners 64 + 8 t ..
+__device__ __forceinline__ int rope_row(int d) { return 16 * (d >> 3) + (d & 7); }
+
 // silu(g) * u with the rounding of the torch ops it replaces: g and u rounded to fp16, silu evaluated in fp32 as
 // g / (1 + exp(-g)) and rounded, the product rounded
 __device__ __forceinline__ f16 silu_mul(float g, float u) {

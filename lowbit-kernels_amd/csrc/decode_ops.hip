@@ -59,13 +59,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16* __restrict__ x,
 
 // qkv [M][(Hq + 2 Hkv) D] (the fused projection's output, bias included) -> q_out [M][Hq][D] with RoPE; k (with
 // RoPE) and v written to k_cache / v_cache [Hkv][L][D] at row positions[m]. One thread per (token, head, dim pair
-// (i, i + 64)). RoPE as transformers computes it for fp16 models: angle = fp32(position * inv_freq[i]), cos and sin
-// in fp32 rounded to fp16, x * cos + rotate_half(x) * sin with each product and the sum rounded to fp16.
+// (i, i + 64)), RoPE by rope_pair. permuted: qkv holds each head's rows in the RoPE-permuted order (rope_row), as the
+// fused decoder's W4A16 q|k|v projection writes them.
 __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qkv, const int64_t* __restrict__ pos,
                                                       const float* __restrict__ inv_freq, f16* __restrict__ q_out,
                                                       f16* __restrict__ k_cache, f16* __restrict__ v_cache, int M,
-                                                      int Hq, int Hkv, int L) {
-#pragma clang fp contract(off)                                 // each product rounded to fp16 before the sum, as torch
+                                                      int Hq, int Hkv, int L, bool permuted) {
   const int heads = Hq + 2 * Hkv;
   const int gid = blockIdx.x * blockDim.x + threadIdx.x;
   const int i = gid & 63, h = (gid >> 6) % heads, m = (gid >> 6) / heads;
@@ -73,17 +72,15 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
   const int64_t p = pos[m];
   if (p < 0 || p >= L) return;                               // the host checks positions; never write out of bounds
   const f16* src = qkv + ((size_t)m * heads + h) * kHeadDim;
+  const int s1 = permuted ? rope_row(i) : i, s2 = permuted ? rope_row(i) + 8 : i + 64;   // dims i and i + 64
   if (h >= Hq + Hkv) {                                       // v: plain copy into the cache
     f16* dst = v_cache + ((size_t)(h - Hq - Hkv) * L + p) * kHeadDim;
-    dst[i] = src[i];
-    dst[i + 64] = src[i + 64];
+    dst[i] = src[s1];
+    dst[i + 64] = src[s2];
     return;
   }
-  const float ang = (float)p * inv_freq[i];
-  const f16 c = (f16)cosf(ang), s = (f16)sinf(ang);
-  const f16 x1 = src[i], x2 = src[i + 64];
-  const f16 o1 = (f16)(x1 * c) + (f16)(-x2 * s);
-  const f16 o2 = (f16)(x2 * c) + (f16)(x1 * s);
+  f16 o1, o2;
+  rope_pair(src[s1], src[s2], p, inv_freq[i], o1, o2);
   f16* dst = h < Hq ? q_out + ((size_t)m * Hq + h) * kHeadDim : k_cache + ((size_t)(h - Hq) * L + p) * kHeadDim;
   dst[i] = o1;
   dst[i + 64] = o2;
@@ -323,10 +320,10 @@ hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, fl
 }
 
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
-                          f16* v_cache, int M, int Hq, int Hkv, int L, hipStream_t st) {
+                          f16* v_cache, int M, int Hq, int Hkv, int L, bool permuted, hipStream_t st) {
   const long threads = (long)M * (Hq + 2 * Hkv) * 64;
   return launch(rope_kv_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, qkv, pos, inv_freq, q_out,
-                k_cache, v_cache, M, Hq, Hkv, L);
+                k_cache, v_cache, M, Hq, Hkv, L, permuted);
 }
 
 namespace {

@@ -275,6 +275,25 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   for (int d = 0; d < D - 1; ++d)
     if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
 
+  // RoPE epilogue (M = 1): rows n (dim d of a head) and n + 8 (dim d + 64) -> bias, RoPE, q_out or the caches
+  auto rope_store = [&](int n, float v1, float v2) {
+    const RopeArgs& ra = epi.rope;
+    const int64_t p = ra.pos[0];
+    if (p < 0 || p >= ra.L) return;                         // the host checks positions; never write out of bounds
+    const f16 x1 = (f16)v1 + epi.aux[n], x2 = (f16)v2 + epi.aux[n + 8];
+    const int hh = n >> 7, pj = n & 127, d = 8 * (pj >> 4) + (pj & 7);
+    if (hh >= ra.Hq + ra.Hkv) {
+      f16* dst = ra.v_cache + ((size_t)(hh - ra.Hq - ra.Hkv) * ra.L + p) * 128;
+      dst[d] = x1;
+      dst[d + 64] = x2;
+      return;
+    }
+    f16 o1, o2;
+    rope_pair(x1, x2, p, ra.inv_freq[d], o1, o2);
+    f16* dst = hh < ra.Hq ? ra.q_out + (size_t)hh * 128 : ra.k_cache + ((size_t)(hh - ra.Hq) * ra.L + p) * 128;
+    dst[d] = o1;
+    dst[d + 64] = o2;
+  };
   if (nwaves == 1) {                                        // no split of K: the quad sums are the outputs
 #pragma unroll
     for (int i = 0; i < R; ++i)
@@ -282,9 +301,12 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       for (int m = 0; m < M; ++m) {
         const float v = quad_sum(acc[i][m]);
         const int n = 16 * (t0 + i) + r;
-        if (kFused && epi.mode == kEpiSiluMul) {            // row r + 8 (the up row) sits 32 lanes on
+        if (kFused && (epi.mode == kEpiSiluMul || epi.mode == kEpiRopeQKV)) {   // row r + 8 sits 32 lanes on
           const float up = shfl_down32(v);
-          if (q == 0 && r < 8 && n < N) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
+          if (q == 0 && r < 8 && n < N) {
+            if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
+            else rope_store(n, v, up);
+          }
         } else if (q == 0 && n < N) {
           y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
         }
@@ -304,14 +326,15 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   for (int idx = threadIdx.x; idx < R * M * 16; idx += blockDim.x) {
     const int i = idx / (M * 16), m = (idx / 16) % M, rr = idx % 16;
     const int n = 16 * (t0 + i) + rr;
-    if (kFused && epi.mode == kEpiSiluMul) {
+    if (kFused && (epi.mode == kEpiSiluMul || epi.mode == kEpiRopeQKV)) {
       if (rr >= 8 || n >= N) continue;
       float g = 0.f, u = 0.f;
       for (int wv2 = 0; wv2 < nwaves; ++wv2) {
         g += red[wv2 * (R * M * 16) + idx];
         u += red[wv2 * (R * M * 16) + idx + 8];
       }
-      y[(size_t)m * (N / 2) + 8 * (t0 + i) + rr] = silu_mul(g, u);
+      if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + rr] = silu_mul(g, u);
+      else rope_store(n, g, u);
       continue;
     }
     float v = 0.f;

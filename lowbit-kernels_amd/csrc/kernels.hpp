@@ -11,10 +11,23 @@ namespace lowbit {
 //   kEpiResidual  y[m][n] = residual[m][n] + fp16(acc)                   (aux = residual [M][N]; may be y itself)
 //   kEpiSiluMul   rows interleaved 8 gate, 8 up per 16-row tile; y [M][N/2] = silu(fp16(gate)) * fp16(up),
 //                 output column 8 t + r for gate row 16 t + r, up row 16 t + 8 + r
-enum : int { kEpiStore = 0, kEpiBias = 1, kEpiResidual = 2, kEpiSiluMul = 3 };
+//   kEpiRopeQKV   (one row, GEMV only) the q|k|v projection of a decoder layer with its rows permuted per 128-row head
+//                 so that tile j holds dims 8 j .. 8 j + 7 and 64 + 8 j .. 64 + 8 j + 7: fp16(acc) + aux[n] (bias),
+//                 then RoPE at rope.pos[0] on q and k heads; q -> rope.q_out [Hq][128], k and v -> the caches' row
+//                 pos (as lowbit_rope_kv on the unfused, unpermuted output)
+enum : int { kEpiStore = 0, kEpiBias = 1, kEpiResidual = 2, kEpiSiluMul = 3, kEpiRopeQKV = 4 };
+struct RopeArgs {
+  const int64_t* pos = nullptr;
+  const float* inv_freq = nullptr;
+  f16* q_out = nullptr;
+  f16* k_cache = nullptr;
+  f16* v_cache = nullptr;
+  int Hq = 0, Hkv = 0, L = 0;
+};
 struct Epilogue {
   int mode = kEpiStore;
   const f16* aux = nullptr;
+  RopeArgs rope;
 };
 
 struct GemvArgs {
@@ -112,7 +125,7 @@ PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes);
 hipError_t gemm_prefill_launch(const GemvArgs& a, void* workspace, size_t workspace_bytes);
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st);
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
-                          f16* v_cache, int M, int Hq, int Hkv, int L, hipStream_t st);
+                          f16* v_cache, int M, int Hq, int Hkv, int L, bool permuted, hipStream_t st);
 hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st);
 hipError_t hbm_read_launch(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t stream);
 hipError_t hbm_copy_launch(const void* src, void* dst, size_t bytes, int blocks, hipStream_t stream);

@@ -35,7 +35,9 @@ SIGNATURES = {
     "lowbit_w4_gemm_prefill": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, _vp, ctypes.c_size_t, _vp],
                                _int),
     "lowbit_rmsnorm": ([_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp], _int),
-    "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _int),
+    "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
+    "lowbit_w4_qkv_rope": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _i64,
+                            _i64, _i64, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
@@ -283,10 +285,24 @@ class NativeExt:
                                           _stream(x.device)))
         return y
 
-    def rope_kv(self, qkv, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv):
+    def rope_kv(self, qkv, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, permuted=False):
         with _DeviceGuard(qkv.device):
             check(self.lib.lowbit_rope_kv(ptr(qkv), ptr(positions), ptr(inv_freq), ptr(q_out), ptr(k_cache),
-                                          ptr(v_cache), qkv.shape[0], hq, hkv, k_cache.shape[1], _stream(qkv.device)))
+                                          ptr(v_cache), qkv.shape[0], hq, hkv, k_cache.shape[1], int(bool(permuted)),
+                                          _stream(qkv.device)))
+
+    def w4_qkv_rope(self, x, w, s, group, bias, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, norm=None):
+        """One token: the RoPE-permuted q|k|v projection (+ bias, RoPE, cache write) into q_out [1, Hq, 128] and
+        the caches [Hkv, L, 128]; norm = (weight, eps) normalizes x first."""
+        _check_tensors(x, w, s, group)
+        if x.shape[0] != 1:
+            raise RuntimeError("w4_qkv_rope takes one row")
+        nw, eps = norm if norm is not None else (None, 0.0)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_w4_qkv_rope(ptr(x), ptr(w), ptr(s), w.shape[0], x.shape[1], group, ptr(bias),
+                                              ptr(nw) if nw is not None else None, float(eps), ptr(positions),
+                                              ptr(inv_freq), ptr(q_out), ptr(k_cache), ptr(v_cache), hq, hkv,
+                                              k_cache.shape[1], _stream(x.device)))
 
     def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale, split=True):
         """split=False runs one block per (token, head group), without the key partitions and their workspace."""

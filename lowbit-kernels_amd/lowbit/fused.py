@@ -7,7 +7,9 @@ small launch costs ~3 us, that overhead, not the projections, dominates a decode
     rmsnorm -> qkv projection (+bias) -> rope + cache write -> attention -> o projection (+residual, in place)
     -> rmsnorm -> gate|up projection (silu(gate) * up) -> down projection (+residual, in place)
 
-(for one token with W4A16 projections the two RMSNorms run inside the q|k|v and gate|up GEMVs' prologues: 7 launches)
+(for one token with W4A16 projections the two RMSNorms run inside the q|k|v and gate|up GEMVs' prologues and RoPE +
+cache write inside the q|k|v store, whose rows are permuted per head so that rotation partners share a tile: 6
+launches, the attention's partition merge included)
 
 with its own KV cache. The projections are either W4A16 (lowbit_w4_linear_fused: GEMV / MFMA kernels with the
 consumer fused into the store, for up to 64 rows; dequantize + hipBLASLt beyond) or fp16 (hipBLASLt through torch,
@@ -33,6 +35,16 @@ def interleave_gate_up(gate, up):
         raise ValueError("gate and up need the same row count, a multiple of 8")
     rest = gate.shape[1:]
     return torch.stack([gate.reshape(i // 8, 8, *rest), up.reshape(i // 8, 8, *rest)], 1).reshape(2 * i, *rest)
+
+
+def rope_permutation(heads, head_dim=128):
+    """Row order of a q|k|v projection for the fused RoPE: within each head, 16-row tile t holds dims 8 t .. 8 t + 7
+    then their rotation partners head_dim / 2 + 8 t .. (row 16 (d / 8) + d % 8 holds dim d < head_dim / 2)."""
+    half = head_dim // 2
+    within = []
+    for t in range(half // 8):
+        within += [8 * t + r for r in range(8)] + [half + 8 * t + r for r in range(8)]
+    return torch.tensor([h * head_dim + d for h in range(heads) for d in within], dtype=torch.long)
 
 
 class _W4:
@@ -105,6 +117,9 @@ class FusedQwen2:
             att, mlp = layer.self_attn, layer.mlp
             qkv_w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).detach()
             qkv_b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).detach().half().contiguous()
+            if quant == "int4":                               # rows in the fused RoPE's order (rope_permutation)
+                perm = rope_permutation(self.hq + 2 * self.hkv, self.head_dim).to(qkv_w.device)
+                qkv_w, qkv_b = qkv_w[perm], qkv_b[perm].contiguous()
             gu_w = interleave_gate_up(mlp.gate_proj.weight.detach(), mlp.up_proj.weight.detach())
             ws = {"qkv": qkv_w, "o": att.o_proj.weight.detach(), "gu": gu_w, "down": mlp.down_proj.weight.detach()}
             if quant == "int4":
@@ -146,12 +161,15 @@ class FusedQwen2:
         attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
         fuse = m == 1 and self.quant == "int4" and self.hidden <= 16384
         for i, lay in enumerate(self.layers):
-            if fuse:                                          # RMSNorm inside the projection's prologue
-                qkv = lay["qkv"](h, EPI_BIAS, lay["qkv"].bias, norm=(lay["in_norm"], self.eps))
+            if fuse:                                          # RMSNorm in the prologue, RoPE + cache write in the store
+                wq = lay["qkv"].wq
+                ext.w4_qkv_rope(h, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, self.inv_freq, q,
+                                self.k_cache[i], self.v_cache[i], self.hq, self.hkv, norm=(lay["in_norm"], self.eps))
             else:
                 ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
                 qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
-            ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
+                ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv,
+                            permuted=self.quant == "int4")
             ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
                           self.scale)
             lay["o"](attn, EPI_RESIDUAL, h, out=h)

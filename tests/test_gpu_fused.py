@@ -121,6 +121,54 @@ def test_rope_and_cache_write_match_transformers(cuda):
     assert int(torch.count_nonzero(k_cache[:, rest])) == 0 and int(torch.count_nonzero(v_cache[:, rest])) == 0
 
 
+def test_rope_kv_permuted_layout_equals_unpermuted(cuda):
+    hq, hkv, L = 16, 2, 96
+    g = torch.Generator(device="cuda").manual_seed(8)
+    inv_freq = decode.random_model("tiny", seed=2).model.rotary_emb.inv_freq.float()
+    pos = torch.tensor([3, 50, 95], device="cuda")
+    qkv = torch.randn(3, (hq + 2 * hkv) * 128, generator=g, device="cuda").half()
+    perm = fused.rope_permutation(hq + 2 * hkv).cuda()
+    outs = []
+    for src, permuted in ((qkv, False), (qkv[:, perm].contiguous(), True)):
+        q = torch.empty(3, hq, 128, dtype=torch.half, device="cuda")
+        kc, vc = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda"), torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+        ops.ext().rope_kv(src, pos, inv_freq, q, kc, vc, hq, hkv, permuted=permuted)
+        outs.append((q, kc, vc))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("hq,hkv,k", [(2, 1, 256), (16, 2, 2048), (12, 2, 1536)])
+def test_qkv_rope_equals_projection_then_rope(cuda, hq, hkv, k):
+    """lowbit_w4_qkv_rope (RMSNorm, q|k|v GEMV, bias, RoPE, cache write in one launch) gives the same bits as the
+    fused-norm projection with the bias epilogue followed by lowbit_rope_kv on the permuted layout."""
+    n, L = (hq + 2 * hkv) * 128, 64
+    wq, _, *_, gen = make_weight(k, n, k + n, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    nw = (1 + 0.1 * torch.randn(k, generator=gen)).half().cuda()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    for p in (0, 37, 63, 64):
+        x = (torch.randn(1, k, generator=gen) * 3).half().cuda()
+        pos = torch.tensor([p], device="cuda")
+        caches = []
+        for fused_call in (False, True):
+            q = torch.zeros(1, hq, 128, dtype=torch.half, device="cuda")
+            kc = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+            vc = torch.zeros_like(kc)
+            if fused_call:
+                ext.w4_qkv_rope(x, wq.packed_mma, wq.scales, wq.group, bias, pos, inv_freq, q, kc, vc, hq, hkv,
+                                norm=(nw, 1e-6))
+            else:
+                qkv = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias, norm=(nw, 1e-6))
+                ext.rope_kv(qkv, pos, inv_freq, q, kc, vc, hq, hkv, permuted=True)
+            caches.append((q, kc, vc))
+        for a, b in zip(*caches):
+            assert torch.equal(a, b), p
+        if p >= L:                                          # out of the cache: nothing written, q untouched
+            assert int(torch.count_nonzero(caches[1][1])) == 0 and int(torch.count_nonzero(caches[1][0])) == 0
+
+
 @pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
                                                 (28, 4, 300, list(range(200, 248))), (2, 1, 64, [10, 40]),
                                                 (16, 2, 4096, [4095]), (28, 4, 2048, [5, 2047]),

@@ -41,3 +41,16 @@ def test_random_model_is_seeded_and_scaled():
     wa = a.model.layers[0].mlp.down_proj.weight.float()
     assert torch.equal(wa, b.model.layers[0].mlp.down_proj.weight.float())
     assert abs(float(wa.std()) - 0.02) < 2e-3 and float(a.model.layers[0].self_attn.q_proj.bias.abs().max()) == 0.0
+
+
+def test_rope_permutation_pairs_rotation_partners_in_one_tile():
+    """Row 16 (d / 8) + d % 8 of each head holds dim d < 64 and the row 8 below it holds d + 64 (the kernels'
+    rope_row), and the permutation is a bijection of every head's 128 rows."""
+    from lowbit import fused
+    heads = 5
+    perm = fused.rope_permutation(heads).tolist()
+    assert sorted(perm) == list(range(heads * 128))
+    for h in range(heads):
+        for d in range(64):
+            row = 16 * (d // 8) + d % 8
+            assert perm[h * 128 + row] == h * 128 + d and perm[h * 128 + row + 8] == h * 128 + d + 64
