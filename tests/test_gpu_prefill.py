@@ -140,3 +140,15 @@ def test_prefill_every_launch_shape(cuda, k, n, m):
                     assert_rounds(prefill(x, wq), ref16)
     finally:
         _native.lib().lowbit_set_launch_override(0, 0, 0)
+
+
+@pytest.mark.parametrize("k,n,m,g", [(512, 4096, 130, 256), (1024, 1000, 200, 512), (18944, 512, 100, 256)])
+def test_prefill_group_sizes(cuda, k, n, m, g):
+    """Groups spanning several 128-k chunks (one scale per 2 or 4 chunks), with K splits whose boundaries fall inside
+    a group on the long-K case."""
+    wq, ref_w, *_, gen = make_weight(k, n, k + n + g, group=g, layouts=("mma",), sd=0.02)
+    x = torch.randn(m, k, generator=gen).half().cuda()
+    y = prefill(x, wq)
+    ref = x.double() @ ref_w.t()
+    assert rel(y, ref) < bound(x, ref_w, ref)
+    assert_rounds(y, x.double() @ ops.dequant(wq, "mma").double().t())
