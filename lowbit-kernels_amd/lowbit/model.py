@@ -16,8 +16,9 @@ TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down
 
 
 class W4Linear(nn.Module):
-    """nn.Linear replacement holding an ops.W4Weight. forward flattens the leading dimensions, runs ops.linear in fp16
-    (GEMV / MFMA / dequantize + BLAS by row count, or a fixed `gemv_version`) and adds the bias in place."""
+    """nn.Linear replacement holding an ops.W4Weight. forward flattens the leading dimensions and runs ops.linear in
+    fp16 (GEMV / MFMA / dequantize + BLAS by row count, or a fixed `gemv_version`) with the bias, which the INT4
+    kernels add in their store (reference lowbit/model.py:25-26 adds it as a separate op; same rounding)."""
 
     def __init__(self, wq, bias, in_features, out_features, gemv_version=0):
         super().__init__()
@@ -30,9 +31,8 @@ class W4Linear(nn.Module):
 
     def forward(self, x):
         lead = x.shape[:-1]
-        y = ops.linear(x.reshape(-1, self.in_features).to(torch.float16), self.wq, version=self.gemv_version)
-        if self.bias is not None:
-            y.add_(self.bias)
+        y = ops.linear(x.reshape(-1, self.in_features).to(torch.float16), self.wq, version=self.gemv_version,
+                       bias=self.bias)
         return y.view(*lead, self.out_features)
 
     def extra_repr(self):

@@ -193,10 +193,12 @@ def prefill_path(m, wq):
     return auto_version(m, wq) is None and wq.packed_mma is not None and wq.k >= AUTO_PREFILL_MIN_K
 
 
-def linear(x, wq, max_gemv_rows=8, version=0):
+def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     """Decode (few rows): an INT4 kernel (v6 GEMV for one row, v5 MFMA beyond). Prefill (many rows): dequantize, then
     the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or on long K the int4 prefill GEMM (prefill_path). version 0 =
-    auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above."""
+    auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above.
+    bias (fp16 [N], optional; not in the reference's signature): y = fp16(x W^T) + bias in fp16, the rounding of the
+    reference's linear() followed by `+ bias`; the v5 / v6 / prefill kernels add it in their store (no extra launch)."""
     m = x.shape[0]
     if m == 0:
         return x.new_empty(0, wq.n)
@@ -206,8 +208,14 @@ def linear(x, wq, max_gemv_rows=8, version=0):
         v = version if m <= (MAX_ROWS[5] if version == 5 else min(max_gemv_rows, MAX_ROWS[version])) else None
     else:
         raise ValueError(f"version must be 0 (auto) or one of {sorted(MAX_ROWS)}")
+    if bias is not None and v in (5, 6):
+        return ext().w4_linear_fused(x.contiguous(), wq.packed_mma, wq.scales, wq.group, _native.EPI_BIAS, bias)
     if v is not None:
-        return gemv(x, wq, v)
-    if version == 0 and prefill_path(m, wq):
-        return prefill(x, wq)
-    return torch.nn.functional.linear(x, dequant(wq, "mma" if wq.packed_mma is not None else "canonical"))
+        y = gemv(x, wq, v)
+    elif version == 0 and prefill_path(m, wq):
+        if bias is not None:
+            return ext().w4_gemm_prefill(x.contiguous(), wq.packed_mma, wq.scales, wq.group, _native.EPI_BIAS, bias)
+        y = prefill(x, wq)
+    else:
+        y = torch.nn.functional.linear(x, dequant(wq, "mma" if wq.packed_mma is not None else "canonical"))
+    return y.add_(bias) if bias is not None else y

@@ -240,3 +240,14 @@ def test_fused_qwen2_matches_transformers(cuda, tiny_models):
     for got in (got4, got1):
         err4 = float((got - ref4).abs().max() / ref4.pow(2).mean().sqrt())
         assert err4 < 2e-2, err4
+
+
+@pytest.mark.parametrize("k,n", [(1024, 2560), (16384, 512)])
+def test_linear_with_bias_equals_linear_then_add(cuda, k, n):
+    """ops.linear's bias (the GEMV, MFMA and prefill kernels add it in their store) gives the bits of linear() then
+    `+ bias`, the reference W4Linear's two ops, on every route: v6, v5, dequantize + BLAS, and the long-K prefill."""
+    wq, _, *_, gen = make_weight(k, n, k + n, layouts=("mma",), sd=0.05)
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    for m in (1, 3, 16, 64, 96):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        assert torch.equal(ops.linear(x, wq, bias=bias), ops.linear(x, wq) + bias), (k, n, m)
