@@ -53,12 +53,14 @@ const char* lowbit_strerror(int status);
 /* Library version string. */
 const char* lowbit_version(void);
 
-/* Process-wide launch-shape override of the two MFMA-layout kernels, for tuning sweeps. waves_per_group: the M <= 8
- * GEMV's waves per workgroup (0 = automatic, else 1, 2, 4, 8 or 16; clamped to what the register budget allows).
- * ring: chunk slots in flight per wave (0 = automatic, else 2, 3, 4 or 8: the GEMV uses 4 or 8, 8 only for M <= 2;
- * the MFMA GEMM uses 2, 3 or 4). k_splits: workgroups the MFMA GEMM splits K over (0 = automatic, 1..32; bounded by
- * the workspace and by K / 256). Affects later launches only. No counterpart in the reference (its launch shapes
- * were compile-time template choices). */
+/* Process-wide launch-shape override of the MFMA-layout kernels, for tuning sweeps. waves_per_group: the M <= 8
+ * GEMV's waves per workgroup (0 = automatic, else 1, 2, 4, 8 or 16; clamped to what the register budget allows); for
+ * the prefill GEMM the tile shape (1: 64 activation rows / 4 waves, 2: 64 / 8 waves, 4: 128 / 4 waves, 8: 128 / 8
+ * waves, which is never built and falls back to 4 waves). ring: chunk slots in flight per wave (0 = automatic, else
+ * 2, 3, 4 or 8: the GEMV uses 4 or 8, 8 only for M <= 2; the MFMA GEMM 2, 3 or 4; the prefill GEMM 2 or 3, and 4 =
+ * 2 with a two-chunk activation lookahead). k_splits: workgroups the MFMA and prefill GEMMs split K over
+ * (0 = automatic, 1..32; bounded by the workspace and by K / 128). Affects later launches only. No counterpart in
+ * the reference (its launch shapes were compile-time template choices). */
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
