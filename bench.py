@@ -78,6 +78,8 @@ def parse():
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
                     help="with --e2e MODEL: build only that variant, prefill, capture one step and replay --steps greedy "
                          "tokens (a profiler workload; prints nothing else)")
+    ap.add_argument("--chunk", type=int, default=1,
+                    help="with --decode-trace: tokens fed per captured step (1 = greedy decoding)")
     ap.add_argument("--out", default=None)
     return ap.parse_args()
 
@@ -631,16 +633,17 @@ def decode_trace(a):
     cfg = E2E[a.e2e]
     torch.cuda.set_device(0)
     m = decode.random_model(a.e2e, seed=0)
-    steps = min(a.steps, 256)
-    max_len = cfg["prompt"] + steps + 64
+    steps, chunk = min(a.steps, 256), a.chunk
+    max_len = cfg["prompt"] + steps * chunk + 64
     clip = CLIP_GRID if cfg["clip"] else None
     if a.decode_trace.startswith("fused"):
-        dec = fused.FusedDecoder(fused.FusedQwen2(m, max_len, quant=a.decode_trace.split("_")[1], clip_grid=clip))
+        dec = fused.FusedDecoder(fused.FusedQwen2(m, max_len, quant=a.decode_trace.split("_")[1], clip_grid=clip),
+                                 chunk)
         del m
     else:
         if a.decode_trace == "hf_int4":
             lbmodel.apply_int4(lbmodel.quantize_layers(m, GROUP, clip))
-        dec = decode.GraphDecoder(m, max_len, 1)
+        dec = decode.GraphDecoder(m, max_len, chunk)
     torch.cuda.empty_cache()
     vocab = decode.qwen25_config(a.e2e).vocab_size
     prompt = torch.randint(0, vocab, (1, cfg["prompt"]), generator=torch.Generator(device="cuda").manual_seed(2024),
@@ -649,10 +652,18 @@ def decode_trace(a):
     dec.capture()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    dec.greedy(first, steps)
+    if chunk == 1:
+        dec.greedy(first, steps)
+        tokens = steps - 1
+    else:
+        feed = torch.randint(0, vocab, (steps * chunk,), generator=torch.Generator(device="cuda").manual_seed(7),
+                             device="cuda")
+        for i in range(steps):
+            dec.step(feed[i * chunk:(i + 1) * chunk])
+        tokens = steps * chunk
     torch.cuda.synchronize()
-    print(json.dumps({"decode_trace": a.decode_trace, "e2e": a.e2e, "steps": steps,
-                      "ms_per_token": round(1000 * (time.perf_counter() - t0) / (steps - 1), 4)}), flush=True)
+    print(json.dumps({"decode_trace": a.decode_trace, "e2e": a.e2e, "steps": steps, "chunk": chunk,
+                      "ms_per_token": round(1000 * (time.perf_counter() - t0) / tokens, 4)}), flush=True)
 
 
 def main():

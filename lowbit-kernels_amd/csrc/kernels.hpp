@@ -89,6 +89,7 @@ constexpr int kAttnTargetBlocks = 256;
 constexpr int kAttnMinKeys = 64;
 constexpr int kAttnMinSplitKeys = 512;
 constexpr int kAttnMaxParts = 16;
+constexpr int kAttnManyBlocks = 512;      // from this many blocks on, at most 4 waves per block
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
 // (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
