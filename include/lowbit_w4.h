@@ -59,8 +59,11 @@ const char* lowbit_version(void);
  * waves, which is never built and falls back to 4 waves). ring: chunk slots in flight per wave (0 = automatic, else
  * 2, 3, 4 or 8: the GEMV uses 4 or 8, 8 only for M <= 2; the MFMA GEMM 2, 3 or 4; the prefill GEMM 2 or 3, and 4 =
  * 2 with a two-chunk activation lookahead). k_splits: workgroups the MFMA and prefill GEMMs split K over
- * (0 = automatic, 1..32; bounded by the workspace and by K / 128). Affects later launches only. No counterpart in
- * the reference (its launch shapes were compile-time template choices). */
+ * (0 = automatic, 1..32; bounded by the workspace and by K / 128); for the M <= 8 GEMV, workgroups sharing one
+ * 16-row tile (1, 2 or 4, owning 16, 8 or 4 rows each; honoured with one tile per wave, K / 128 a multiple of it and
+ * no silu-mul or RoPE epilogue, which pair rows r and r + 8; other values leave the GEMV's choice automatic).
+ * Affects later launches only. No counterpart in the reference (its launch shapes were compile-time template
+ * choices). */
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.

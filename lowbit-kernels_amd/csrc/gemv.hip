@@ -49,13 +49,18 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 // refilled as soon as it is consumed. Weight loads use one buffer resource per tile: chunks past K and rows past N
 // read as zero without a branch, so the compiler waits on exactly the slot it needs. When M K is too large for LDS
 // (kLdsX = false) each lane loads its x pairs from global memory and decodes exactly.
-template <int M, int R, int D, bool kLdsX, bool kFused = false>
+// CS > 1 (R = 1) splits each 16-row tile over CS workgroups of 16 / CS rows, so layers with few tiles still occupy
+// every CU: a wave-load then covers CS consecutive chunks of the workgroup's rows (lane l: chunk l / (64 / CS)), each
+// piece a contiguous 64 * 16 / CS bytes, and the CS partial sums of a row are added across lanes before the waves'.
+template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
                                                                            f16* y, int N, int K, int G,
                                                                            Epilogue epi,
                                                                            const f16* __restrict__ norm_w, float eps) {
+  static_assert(CS == 1 || (R == 1 && (CS == 2 || CS == 4)), "a tile splits over 2 or 4 workgroups, one tile each");
+  constexpr int RS = 16 / CS;                               // rows of a tile one workgroup owns
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   // norm_w (M = 1 with x in LDS only; the launcher then gives every block of x a thread): the projection's input is
   // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
@@ -64,11 +69,14 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
-  const int r = lane >> 2, q = lane & 3;
+  const int q = lane & 3, rl = (lane >> 2) & (RS - 1), cs = lane / (4 * RS);   // cs: chunk within a wave-load
+  const int sub = CS == 1 ? 0 : (int)blockIdx.x % CS;      // which 16 / CS rows of the tile
+  const int r = RS * sub + rl;                              // this lane's row within its 16-row tile
   const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
   const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
-  const int t0 = blockIdx.x * R;
-  const int n0 = 16 * t0, nrows = min(16 * R, N - n0);    // rows of this workgroup
+  const int t0 = (CS == 1 ? (int)blockIdx.x : (int)blockIdx.x / CS) * R;
+  const int n0 = 16 * t0 + RS * sub, nrows = min(RS * R, N - n0);   // rows of this workgroup
+  if (nrows <= 0) return;                                  // a row split past the last row of a narrow tile
   // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16
   f16* lds_x = reinterpret_cast<f16*>(smem);
   float* lds_xs = reinterpret_cast<float*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
@@ -116,9 +124,9 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     const int rows = t0 + i < ntiles ? min(16, N - 16 * t) : 0;
     const bool live = r < rows;
     wr[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
-    woff[i] = live ? 64 * r + 16 * q : kOutOfRange;
-    wstep[i] = live ? rows * 64 : 0;                       // bytes from one chunk to the next inside the tile
-    srow[i] = live ? (16 * i + r) * KG : 0;                // this lane's row in the staged scales
+    woff[i] = live ? 64 * r + 16 * q + cs * rows * 64 : kOutOfRange;
+    wstep[i] = live ? CS * rows * 64 : 0;                  // bytes from one wave-load's chunks to the next
+    srow[i] = live ? (16 * i + rl) * KG : 0;               // this lane's row in the staged scales
   }
   u32x4 ring[D][R];
 #pragma unroll
@@ -209,11 +217,13 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
 
-  // this wave's chunks are c_j = wave + j * nwaves, j < nj. Full groups of D refill their slot D chunks ahead (past
-  // the end the refill reads zeros); the last partial group drains the ring without refills.
-  const int nj = (KC - wave + nwaves - 1) / nwaves;
+  // this wave's wave-loads are c_j = wave + j * nwaves, j < nj (wave-load c holds chunks CS c .. CS c + CS - 1). Full
+  // groups of D refill their slot D wave-loads ahead (past the end the refill reads zeros); the last partial group
+  // drains the ring without refills.
+  const int nj = (KC / CS - wave + nwaves - 1) / nwaves;
   const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
-  auto consume = [&](const u32x4 (&slot)[R], int c) {
+  auto consume = [&](const u32x4 (&slot)[R], int cw) {
+    const int c = CS * cw + cs;                             // this lane's chunk
     const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
     u32x4 xv[M][4];
     if (kLdsX) {
@@ -294,6 +304,17 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     dst[d] = o1;
     dst[d + 64] = o2;
   };
+  if constexpr (CS > 1) {                                   // the CS chunks of a wave-load: lanes 64 / CS apart
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        acc[i][m] += __shfl_xor(acc[i][m], 32, 64);
+        if (CS == 4) acc[i][m] += __shfl_xor(acc[i][m], 16, 64);
+      }
+  }
+  // silu-mul and RoPE pair row r with row r + 8 of the tile, which one workgroup holds only when CS = 1
+  const bool pairs = kFused && CS == 1 && (epi.mode == kEpiSiluMul || epi.mode == kEpiRopeQKV);
   if (nwaves == 1) {                                        // no split of K: the quad sums are the outputs
 #pragma unroll
     for (int i = 0; i < R; ++i)
@@ -301,13 +322,13 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       for (int m = 0; m < M; ++m) {
         const float v = quad_sum(acc[i][m]);
         const int n = 16 * (t0 + i) + r;
-        if (kFused && (epi.mode == kEpiSiluMul || epi.mode == kEpiRopeQKV)) {   // row r + 8 sits 32 lanes on
+        if (pairs) {                                        // row r + 8 sits 32 lanes on
           const float up = shfl_down32(v);
           if (q == 0 && r < 8 && n < N) {
             if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
             else rope_store(n, v, up);
           }
-        } else if (q == 0 && n < N) {
+        } else if (q == 0 && cs == 0 && n < N) {
           y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
         }
       }
@@ -320,25 +341,25 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const float v = quad_sum(acc[i][m]);
-      if (q == 0) red[wave * (R * M * 16) + (i * M + m) * 16 + r] = v;
+      if (q == 0 && cs == 0) red[wave * (R * M * RS) + (i * M + m) * RS + rl] = v;
     }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < R * M * 16; idx += blockDim.x) {
-    const int i = idx / (M * 16), m = (idx / 16) % M, rr = idx % 16;
-    const int n = 16 * (t0 + i) + rr;
-    if (kFused && (epi.mode == kEpiSiluMul || epi.mode == kEpiRopeQKV)) {
+  for (int idx = threadIdx.x; idx < R * M * RS; idx += blockDim.x) {
+    const int i = idx / (M * RS), m = (idx / RS) % M, rr = idx % RS;
+    const int n = 16 * (t0 + i) + RS * sub + rr;
+    if (pairs) {
       if (rr >= 8 || n >= N) continue;
       float g = 0.f, u = 0.f;
       for (int wv2 = 0; wv2 < nwaves; ++wv2) {
-        g += red[wv2 * (R * M * 16) + idx];
-        u += red[wv2 * (R * M * 16) + idx + 8];
+        g += red[wv2 * (R * M * RS) + idx];
+        u += red[wv2 * (R * M * RS) + idx + 8];
       }
       if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + rr] = silu_mul(g, u);
       else rope_store(n, g, u);
       continue;
     }
     float v = 0.f;
-    for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * 16) + idx];
+    for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * RS) + idx];
     if (n < N) y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
   }
 }
@@ -396,10 +417,10 @@ __global__ __launch_bounds__(256) void gemv_rowmajor(const f16* __restrict__ x, 
 
 namespace {
 
-template <int M, int R, int D>
+template <int M, int R, int D, int CS = 1>
 hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
-  dim3 grid((ntiles + R - 1) / R), block(64 * waves);
+  dim3 grid(CS == 1 ? (ntiles + R - 1) / R : ntiles * CS), block(64 * waves);
   const size_t s_bytes = (size_t)16 * R * (a.K / a.G) * 2;
   const size_t x_bytes = (size_t)M * a.K * 2 + (size_t)M * (a.K / 32) * 8;
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
@@ -407,24 +428,26 @@ hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   if constexpr (M == 1) {                                    // only the M = 1 path carries epilogues and the norm
     if (fused) {
       if (x_bytes + s_bytes <= kGemvLdsX)
-        return launch(gemv_mfma_layout<M, R, D, true, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes),
+        return launch(gemv_mfma_layout<M, R, D, true, true, CS>, grid, block, std::max(x_bytes + s_bytes, red_bytes),
                       a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
       if (a.norm_w) return hipErrorInvalidValue;             // the fused norm needs x in LDS (the C ABI checks K)
-      return launch(gemv_mfma_layout<M, R, D, false, true>, grid, block, std::max(s_bytes, red_bytes), a.stream,
+      return launch(gemv_mfma_layout<M, R, D, false, true, CS>, grid, block, std::max(s_bytes, red_bytes), a.stream,
                     a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
     }
   } else {
     if (fused) return hipErrorInvalidValue;                   // callers send M >= 2 with an epilogue to the MFMA GEMM
   }
   if (x_bytes + s_bytes <= kGemvLdsX)
-    return launch(gemv_mfma_layout<M, R, D, true>, grid, block, std::max(x_bytes + s_bytes, red_bytes), a.stream,
-                  a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
-  return launch(gemv_mfma_layout<M, R, D, false>, grid, block, std::max(s_bytes, red_bytes), a.stream,
+    return launch(gemv_mfma_layout<M, R, D, true, false, CS>, grid, block, std::max(x_bytes + s_bytes, red_bytes),
+                  a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+  return launch(gemv_mfma_layout<M, R, D, false, false, CS>, grid, block, std::max(s_bytes, red_bytes), a.stream,
                 a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
 }
 
 template <int M>
-hipError_t dispatch_mfma_layout(const GemvArgs& a, int R, int waves, int D) {
+hipError_t dispatch_mfma_layout(const GemvArgs& a, int R, int waves, int D, int CS) {
+  if (CS == 2) return launch_mfma_layout<M, 1, 4, 2>(a, waves);   // the planner pairs CS > 1 with R = 1, D = 4
+  if (CS == 4) return launch_mfma_layout<M, 1, 4, 4>(a, waves);
   if constexpr (M <= 2) {
     if (D > 4) {
       switch (R) {
@@ -460,23 +483,33 @@ hipError_t dispatch_rowmajor(const GemvArgs& a, int R, bool v3) {
 
 }  // namespace
 
-GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
+GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok) {
   GemvPlan p;
   const int ntiles = (N + 15) / 16, KC = K / 128;
   const GemvOverride o = gemv_override();
   // From the MI355X graph-mode sweep over the Qwen2.5-1.5B/3B and 7B-shaped projections (M = 1): one 16-row tile
-  // per wave always; 8 waves splitting K on narrow layers (16 on long rows), fewer as the tile count grows so that
-  // about 3k waves are in flight; never more waves than 128-k chunks; 4 chunk slots in flight per wave.
+  // per wave always. A layer with at most 128 tiles and K >= 2048 splits each tile over the most workgroups (2 or 4)
+  // that still fit one round of the 256 CUs: the decode ALU work of its busiest CU then halves or quarters (8960 x
+  // 1536: 5.5 -> 4.3 us, 11008 x 2048: 6.1 -> 4.9 us); a split that leaves a CU two workgroups, or a short K, gains
+  // nothing. 8 waves splitting K on narrow and split layers (16 on long rows), fewer as the tile count grows so that
+  // about 3k waves are in flight; never more waves than wave-loads; 4 wave-loads in flight per wave.
   p.R = rows_per_wave ? rows_per_wave : 1;
-  const int blocks = (ntiles + p.R - 1) / p.R;
+  auto split_fits = [&](int cs) { return p.R == 1 && row_split_ok && KC % cs == 0; };
+  if (o.splits == 1 || ((o.splits == 2 || o.splits == 4) && split_fits(o.splits))) {
+    p.CS = o.splits;
+  } else if (KC >= 16) {
+    for (int cs = 4; cs >= 2 && p.CS == 1; cs /= 2)
+      if (split_fits(cs) && ntiles * cs <= 256) p.CS = cs;
+  }
+  const int blocks = p.CS == 1 ? (ntiles + p.R - 1) / p.R : ntiles * p.CS;
   int waves;
-  if (blocks >= 256) {
+  if (p.CS == 1 && blocks >= 256) {
     waves = 1;
     while (waves < 8 && blocks * waves * 2 <= 3072) waves *= 2;
   } else {
-    waves = KC >= 128 ? 16 : 8;
+    waves = KC / p.CS >= 128 ? 16 : 8;
   }
-  while (waves > 1 && waves > KC) waves /= 2;
+  while (waves > 1 && waves > KC / p.CS) waves /= 2;
   if (o.waves > 0) waves = o.waves;
   p.D = ((o.ring == 4 || o.ring == 8) && M <= 2) ? o.ring : 4;
   p.waves = std::min(waves, gemv_max_threads(M, p.R, p.D) / 64);
@@ -486,20 +519,22 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave) {
 int pick_rows_rowmajor(int N, int M) { return N >= 512 ? 4 : (M >= 4 ? 2 : 1); }
 
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
-  GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave);
+  // a tile may split over workgroups unless the epilogue pairs rows r and r + 8 of a tile
+  const bool row_split_ok = a.epi.mode != kEpiSiluMul && a.epi.mode != kEpiRopeQKV;
+  GemvPlan p = plan_gemv_mfma_layout(a.M, a.N, a.K, rows_per_wave, row_split_ok);
   if (a.norm_w) {                                             // every 32-k block of x held by a thread (2 per thread)
     const int need = (a.K / 32 + 127) / 128;
     while (p.waves < need) p.waves *= 2;
   }
   switch (a.M) {
-    case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves, p.D);
-    case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves, p.D);
-    case 3: return dispatch_mfma_layout<3>(a, p.R, p.waves, p.D);
-    case 4: return dispatch_mfma_layout<4>(a, p.R, p.waves, p.D);
-    case 5: return dispatch_mfma_layout<5>(a, p.R, p.waves, p.D);
-    case 6: return dispatch_mfma_layout<6>(a, p.R, p.waves, p.D);
-    case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves, p.D);
-    default: return dispatch_mfma_layout<8>(a, p.R, p.waves, p.D);
+    case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves, p.D, p.CS);
+    case 2: return dispatch_mfma_layout<2>(a, p.R, p.waves, p.D, p.CS);
+    case 3: return dispatch_mfma_layout<3>(a, p.R, p.waves, p.D, p.CS);
+    case 4: return dispatch_mfma_layout<4>(a, p.R, p.waves, p.D, p.CS);
+    case 5: return dispatch_mfma_layout<5>(a, p.R, p.waves, p.D, p.CS);
+    case 6: return dispatch_mfma_layout<6>(a, p.R, p.waves, p.D, p.CS);
+    case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves, p.D, p.CS);
+    default: return dispatch_mfma_layout<8>(a, p.R, p.waves, p.D, p.CS);
   }
 }
 

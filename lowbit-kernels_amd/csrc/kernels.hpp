@@ -48,6 +48,7 @@ struct GemvPlan {
   int MT = 1;       // 16-column activation tiles (MFMA GEMM)
   int D = 4;        // chunk slots in flight per wave
   int S = 1;        // workgroups splitting K per row group (MFMA GEMM)
+  int CS = 1;       // workgroups sharing a 16-row tile, 16 / CS rows each (MFMA-layout GEMV, R = 1)
 };
 
 // launch shape of the prefill GEMM (M > 64)
@@ -110,7 +111,7 @@ struct ClipGrid {
   float a[kMaxClip];
 };
 
-GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave);
+GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok = true);
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes);
 int pick_rows_rowmajor(int N, int M);
 

@@ -141,7 +141,9 @@ def test_rope_kv_permuted_layout_equals_unpermuted(cuda):
 @pytest.mark.parametrize("hq,hkv,k", [(2, 1, 256), (16, 2, 2048), (12, 2, 1536)])
 def test_qkv_rope_equals_projection_then_rope(cuda, hq, hkv, k):
     """lowbit_w4_qkv_rope (RMSNorm, q|k|v GEMV, bias, RoPE, cache write in one launch) gives the same bits as the
-    fused-norm projection with the bias epilogue followed by lowbit_rope_kv on the permuted layout."""
+    fused-norm projection with the bias epilogue followed by lowbit_rope_kv on the permuted layout. RoPE pairs rows
+    r and r + 8 of a tile, so the fused kernel never splits a tile over workgroups; the two-step reference is pinned
+    to the same unsplit plan (a split would only reorder its fp32 sums)."""
     n, L = (hq + 2 * hkv) * 128, 64
     wq, _, *_, gen = make_weight(k, n, k + n, layouts=("mma",), sd=0.05)
     ext = ops.ext()
@@ -160,7 +162,12 @@ def test_qkv_rope_equals_projection_then_rope(cuda, hq, hkv, k):
                 ext.w4_qkv_rope(x, wq.packed_mma, wq.scales, wq.group, bias, pos, inv_freq, q, kc, vc, hq, hkv,
                                 norm=(nw, 1e-6))
             else:
-                qkv = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias, norm=(nw, 1e-6))
+                _native.check(_native.lib().lowbit_set_launch_override(0, 0, 1))
+                try:
+                    qkv = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias,
+                                              norm=(nw, 1e-6))
+                finally:
+                    _native.check(_native.lib().lowbit_set_launch_override(0, 0, 0))
                 ext.rope_kv(qkv, pos, inv_freq, q, kc, vc, hq, hkv, permuted=True)
             caches.append((q, kc, vc))
         for a, b in zip(*caches):
