@@ -148,6 +148,19 @@ __device__ __forceinline__ f16 silu_mul(float g, float u) {
   return (f16)((float)s * (float)(f16)u);
 }
 
+// Bind kernel arguments to scalar registers at the kernel's start. Kernel arguments are read through the scalar cache,
+// which is cold at every launch (a few hundred ns per round trip); the compiler otherwise fetches each argument at its
+// first use, so a prologue whose later addresses depend on later arguments waits for two or three round trips before
+// its main loads go out. Naming them all here issues every fetch before the first wait.
+template <typename T>
+__device__ __forceinline__ void arg_in_sgpr(const T& v) {
+  asm volatile("" ::"s"(v));
+}
+template <typename... T>
+__device__ __forceinline__ void args_in_sgprs(const T&... v) {
+  (arg_in_sgpr(v), ...);
+}
+
 __device__ __forceinline__ float shfl_down32(float v) {     // lane l gets lane l + 32 (lanes 32..63 get their own)
   return __shfl_down(v, 32, 64);
 }

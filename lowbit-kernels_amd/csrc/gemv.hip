@@ -66,6 +66,8 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
   const bool norm = kFused && kLdsX && M == 1 && norm_w != nullptr;   // kFused: epilogue / norm code compiled in
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  args_in_sgprs(x, w, s, N, K, G, (int)blockDim.x);
+  if constexpr (kFused) args_in_sgprs(epi.aux, norm_w);    // the epilogue's and the norm's argument lines too
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nwaves = blockDim.x >> 6;
@@ -75,8 +77,9 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
   const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
   const int t0 = (CS == 1 ? (int)blockIdx.x : (int)blockIdx.x / CS) * R;
-  const int n0 = 16 * t0 + RS * sub, nrows = min(RS * R, N - n0);   // rows of this workgroup
-  if (nrows <= 0) return;                                  // a row split past the last row of a narrow tile
+  // rows of this workgroup (none for the second half or quarters of a tile cut short by N: such a workgroup reads
+  // only zeros and stores nothing)
+  const int n0 = 16 * t0 + RS * sub, nrows = max(0, min(RS * R, N - n0));
   // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16
   f16* lds_x = reinterpret_cast<f16*>(smem);
   float* lds_xs = reinterpret_cast<float*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
