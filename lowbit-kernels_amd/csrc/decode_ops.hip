@@ -106,6 +106,7 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
     float* __restrict__ part) {
   constexpr int NI = KB / 4;                                 // 16-byte loads per lane and step, per K and per V
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  args_in_sgprs(q, k_cache, v_cache, pos, out, Hq, Hkv, L, CH, part, (int)blockDim.x);
   const int groups = Hq / G, P = gridDim.y, pid = blockIdx.y;
   const int m = blockIdx.x / groups, h0 = (blockIdx.x % groups) * G, hk = h0 / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;

@@ -55,6 +55,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   constexpr int kXBuf = 16 * MT * kXPitch;                 // one staged chunk of x
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_last;
+  args_in_sgprs(x, w, s, y, M, N, K, G, S, ctr, part, epi.aux);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = wave >> 2, tw = wave & 3, gt = tid & 255;  // K-group, tile-wave, thread index inside the K-group

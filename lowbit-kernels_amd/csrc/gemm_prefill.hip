@@ -44,6 +44,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
                                                     float* __restrict__ part, Epilogue epi) {
   constexpr int kXBuf = 16 * MT * 256;                      // one staged chunk of x
   constexpr int kRows = 64 * NW;                            // weight rows per workgroup
+  args_in_sgprs(x, w, s, y, M, N, K, G, S, MG, items, ctr, part, epi.aux);
   constexpr int kThreads = 64 * NW;
   constexpr int XP = 16 * MT * 16 / kThreads;               // 16-byte x pieces per thread and chunk
   static_assert(XP >= 1 && XP * kThreads == 16 * MT * 16, "x pieces must divide evenly");
