@@ -66,6 +66,13 @@ const char* lowbit_version(void);
  * choices). */
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 
+/* Process-wide choice of the MFMA GEMM's structure (lowbit_w4_gemm_mfma, lowbit_w4_linear_fused for M >= 2), for
+ * tuning sweeps and tests: 0 = automatic; 1 = row groups of 64 or 128 weight rows sharing staged activations, K split
+ * across workgroups on narrow layers; 2 = one 16-row tile per workgroup, its waves splitting K (M <= 32 only; larger M
+ * keeps row groups). Results of the two differ only in fp32 summation order. Affects later launches only. No
+ * counterpart in the reference. */
+int lowbit_set_gemm_kernel(int kernel);
+
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
  * Replaces the reference's w4_gemv (csrc/w4_gemv.cu:454-484) and, through it, ops.gemv(version in 1..4, 6)
  * (lowbit/ops.py:67-78). version 1 or 2: w in the canonical layout; 3 or 4: v3 layout; 6: the MFMA layout (needs

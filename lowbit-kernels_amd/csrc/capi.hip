@@ -38,7 +38,7 @@ int check_device() {
   return LOWBIT_OK;
 }
 
-std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0};
+std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0}, g_override_gemm{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -114,6 +114,7 @@ GemvOverride gemv_override() {
   o.waves = g_override_waves.load(std::memory_order_relaxed);
   o.ring = g_override_ring.load(std::memory_order_relaxed);
   o.splits = g_override_splits.load(std::memory_order_relaxed);
+  o.gemm_kernel = g_override_gemm.load(std::memory_order_relaxed);
   return o;
 }
 
@@ -154,6 +155,12 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
   g_override_waves.store(waves_per_group, std::memory_order_relaxed);
   g_override_ring.store(ring, std::memory_order_relaxed);
   g_override_splits.store(k_splits, std::memory_order_relaxed);
+  return ok();
+}
+
+int lowbit_set_gemm_kernel(int kernel) {
+  if (kernel < 0 || kernel > 2) return fail(LOWBIT_ERR_TUNING, "kernel is 0 (auto), 1 (row groups) or 2 (one tile each)");
+  g_override_gemm.store(kernel, std::memory_order_relaxed);
   return ok();
 }
 

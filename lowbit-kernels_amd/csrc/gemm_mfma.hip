@@ -297,6 +297,147 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   }
 }
 
+// gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 32 on layers with few tiles.
+// The row-group kernel above must split K over workgroups there (and pay an agent-scope release per workgroup to add
+// the partials); here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
+// the end, so no workgroup waits for another. Each wave loads, next to its weight piece, the activation piece its B
+// fragments need (lane l: 64 contiguous bytes, x row 16 mt + l % 16, k = 128 c + 32 (l / 16) + [0, 32)) straight into
+// registers: no staging buffer and no barrier inside the K loop. Lane l's weight piece is row l % 16, quarter l / 16
+// (the A fragments of four MFMAs, one coalesced 1 KB wave-load); its scale is row 4 (l / 16) + l % 4, broadcast
+// within the quad to the four D rows the lane holds. Rows past N, chunks past K and activation rows past M read
+// zeros through the buffer bounds.
+template <int MT, int D, int kThreads>
+__global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+                                                        const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
+                                                        Epilogue epi) {
+  args_in_sgprs(x, w, s, y, M, N, K, G, epi.aux, (int)blockDim.x);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+  const int r = lane & 15, q = lane >> 4;
+  const int t = blockIdx.x, n0 = 16 * t;
+  const int rows = min(16, N - n0), KC = K >> 7, KG = K / G, cpg = G >> 7;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)t * 8 * K, (uint32_t)(rows * (K / 2)));
+  const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)N * (uint32_t)KG * 2u);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  const bool wlive = r < rows;
+  const int woff = wlive ? 64 * r + 16 * q : 0, wstep = rows * 64;
+  const int srow = n0 + 4 * q + (r & 3);
+  const bool slive = srow < N;
+  const int soff = slive ? 2 * srow * KG : 0;
+  int xoff[MT];
+  bool xlive[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    xlive[mt] = 16 * mt + r < M;
+    xoff[mt] = xlive[mt] ? ((16 * mt + r) * K + 32 * q) * 2 : 0;
+  }
+  const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
+
+  u32x4 rw[D], rx[D][MT][4];
+  uint32_t rs[D];
+  auto issue = [&](int d, int j) {                          // this wave's j-th chunk into slot d
+    const int c = wave + j * W;
+    const bool live = c < KC;
+    const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
+    rw[d] = buffer_load16_nt(wr, live && wlive ? woff + c * wstep : kOutOfRange);
+    rs[d] = buffer_load2(sr, live && slive ? soff + 2 * g : kOutOfRange);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        rx[d][mt][e] = buffer_load16(xr, live && xlive[mt] ? xoff[mt] + 256 * c + 16 * e : kOutOfRange);
+  };
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const f16x8 a8 = __builtin_bit_cast(f16x8, u32x4{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+  auto consume = [&](int d) {
+    f32x4 pt[MT], xs[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pt[mt] = xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wd = rw[d][j];
+      const f16x8 a = __builtin_bit_cast(
+          f16x8, u32x4{wd & 0x000F000Fu, (wd >> 4) & 0x000F000Fu, (wd >> 8) & 0x000F000Fu, (wd >> 12) & 0x000F000Fu});
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const f16x8 bx = __builtin_bit_cast(f16x8, rx[d][mt][j]);
+        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, bx, xs[mt], 0, 0, 0);
+        pt[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, pt[mt], 0, 0, 0);
+      }
+    }
+    const uint32_t sb = rs[d];
+    const float sc[4] = {(float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<0>(sb)),
+                         (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<1>(sb)),
+                         (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<2>(sb)),
+                         (float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<3>(sb))};
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[mt][v] = fmaf(pt[mt][v] - xs[mt][v], sc[v], acc[mt][v]);
+  };
+
+  // this wave's chunks are wave + j W, j < nj; full groups of D refill their slot D chunks ahead (past the end the
+  // refill reads zeros), the last partial group drains the ring
+  const int nj = (KC - wave + W - 1) / W;
+#pragma unroll
+  for (int d = 0; d < D; ++d) issue(d, d);
+  int j0 = 0;
+  for (; j0 + D <= nj; j0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(d);
+      issue(d, j0 + d + D);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d)
+    if (j0 + d < nj) consume(d);
+
+  // waves 1 .. W-1 hand their sums to wave 0, which adds them in wave order
+  if (W > 1) {
+    f32x4* red = reinterpret_cast<f32x4*>(smem);             // [W - 1][MT][64]
+    if (wave > 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((wave - 1) * MT + mt) * 64 + lane] = acc[mt];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w2 = 1; w2 < W; ++w2)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] += red[((w2 - 1) * MT + mt) * 64 + lane];
+  }
+  // lane (r, q) holds rows n0 + 4 q + v of column m = 16 mt + r
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r, n = n0 + 4 * q;
+    const f32x4 v = acc[mt] * kTwo24;
+    if (epi.mode == kEpiSiluMul) {                          // up rows 8 + 4 q + v sit 32 lanes on (q + 2)
+      const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
+      if (q < 2 && m < M && n < N) {
+        f16* dst = y + (size_t)m * (N / 2) + 8 * (n >> 4) + (n & 15);
+        const f16x2 lo = {silu_mul(v[0], up[0]), silu_mul(v[1], up[1])}, hi = {silu_mul(v[2], up[2]), silu_mul(v[3], up[3])};
+        *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+      }
+      continue;
+    }
+    if (m >= M || n >= N) continue;
+    f16* dst = y + (size_t)m * N + n;
+    if (vec) {
+      const f16x2 lo = {epi_value(epi.mode, epi.aux, v[0], m, n, N), epi_value(epi.mode, epi.aux, v[1], m, n + 1, N)};
+      const f16x2 hi = {epi_value(epi.mode, epi.aux, v[2], m, n + 2, N), epi_value(epi.mode, epi.aux, v[3], m, n + 3, N)};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = epi_value(epi.mode, epi.aux, v[e], m, n + e, N);
+    }
+  }
+}
+
 namespace {
 
 template <int MT, int RW, int D, int KS>
@@ -336,6 +477,17 @@ hipError_t dispatch_ring(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
   }
 }
 
+// one tile per workgroup, up to 8 waves (the register budget of 2 waves per SIMD): M <= 16 with a 4-deep ring, M <= 32
+// with 3 slots
+template <int MT>
+hipError_t launch_tiles(const GemvArgs& a, int waves) {
+  constexpr int D = MT == 1 ? 4 : 3, kThreads = 512;
+  if (waves < 1 || 64 * waves > kThreads) return hipErrorInvalidConfiguration;   // never planned
+  const size_t shmem = (size_t)(waves - 1) * MT * 64 * 16;
+  return launch(gemm_mfma_tiles<MT, D, kThreads>, dim3((a.N + 15) / 16), dim3(64 * waves), shmem, a.stream, a.x, a.w,
+                a.s, a.y, a.M, a.N, a.K, a.G, a.epi);
+}
+
 template <int MT>
 hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
   switch (p.R) {
@@ -346,6 +498,13 @@ hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 
 }  // namespace
 
+// One tile per workgroup beats row groups, from an MI355X sweep (graph-timed, cold weights, M = 2..32 on the
+// Qwen2.5-1.5B/3B/7B projections), on the attention-sized layers: up to 288 tiles (N <= 4608) and K short enough that
+// every wave's own activation loads (4 KB per 1 KB of weights per 16 rows of M) stay cheap, KC * MT <= 32: 1.4-2.4x
+// (2048 x 2560, M = 16: 13.3 -> 5.6 us). Long K (8960 and up) or wide N keep row groups, which share the activations
+// through LDS.
+bool tiles_win(int MT, int ntiles, int KC) { return MT <= 2 && ntiles <= 288 && KC * MT <= 32; }
+
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
 // tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
 // N); K-groups per workgroup until about kGemmTargetWaves waves run; a 3-slot ring for M <= 16 with up to two K-groups,
@@ -355,6 +514,14 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   const GemvOverride o = gemv_override();
   const int ntiles = (N + 15) / 16, KC = K / 128;
   p.MT = (M + 15) / 16;
+  if (p.MT <= 2 && row_tiles == 0 && (o.gemm_kernel == 2 || (o.gemm_kernel == 0 && tiles_win(p.MT, ntiles, KC)))) {
+    int waves = ntiles <= 256 && KC >= 24 ? 8 : 4;            // same sweep
+    if (o.waves > 0) waves = o.waves;
+    waves = std::min(waves, 8);
+    while (waves > 1 && waves > KC) waves /= 2;
+    p.TW = waves;
+    return p;
+  }
   p.R = row_tiles >= 2 ? 2 : 1;
   const int groups = (ntiles + kW * p.R - 1) / (kW * p.R);
   const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
@@ -387,6 +554,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
 
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
   const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
+  if (p.TW > 0) return p.MT == 1 ? launch_tiles<1>(a, p.TW) : launch_tiles<2>(a, p.TW);
   uint32_t* ctr = static_cast<uint32_t*>(workspace);
   float* part = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes) : nullptr;
   switch (p.MT) {

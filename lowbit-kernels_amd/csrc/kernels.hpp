@@ -49,6 +49,7 @@ struct GemvPlan {
   int D = 4;        // chunk slots in flight per wave
   int S = 1;        // workgroups splitting K per row group (MFMA GEMM)
   int CS = 1;       // workgroups sharing a 16-row tile, 16 / CS rows each (MFMA-layout GEMV, R = 1)
+  int TW = 0;       // MFMA GEMM: waves of the one-tile-per-workgroup kernel (0: the row-group kernel)
 };
 
 // launch shape of the prefill GEMM (M > 64)
@@ -67,6 +68,7 @@ struct GemvOverride {
   int waves = 0;
   int ring = 0;
   int splits = 0;
+  int gemm_kernel = 0;  // MFMA GEMM structure: 0 automatic, 1 row groups (K split across workgroups), 2 one tile each
 };
 GemvOverride gemv_override();
 

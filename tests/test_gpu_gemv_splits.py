@@ -2,7 +2,8 @@
 covering 2 or 4 chunks), forced through lowbit_set_launch_override's k_splits, through the C ABI:
 * within the reference's bound of the fp64 product (bench/gpu_run.py:229-245) for every split and wave count, on
   ragged N (a last tile of 8 rows, whose second half-tile workgroups have no rows) and M = 1..8;
-* a split only reorders the fp32 sums: it stays within a few fp16 ulps of the unsplit result;
+* a split only reorders the fp32 sums: within one fp16 ulp of the exact value plus 2^-16 of the output RMS of the
+  unsplit result;
 * bias / residual epilogues and the fused RMSNorm under a split give the same bits as the same split's plain sum plus
   the torch add / the separate norm; silu-mul and RoPE pair rows r and r + 8 of a tile, so they ignore the split."""
 import pytest
@@ -25,8 +26,12 @@ def reset_override():
     _native.check(_native.lib().lowbit_set_launch_override(0, 0, 0))
 
 
-def ulps(a, b):
-    return int((a.view(torch.int16).int() - b.view(torch.int16).int()).abs().max())
+def same_up_to_order(a, b, ref):
+    """|a - b| <= one fp16 ulp of |ref| + 2^-16 RMS(ref): two fp32 summation orders of the same products."""
+    mag = ref.abs().clamp_min(2.0 ** -14)
+    ulp = torch.exp2(torch.floor(torch.log2(mag)) - 10)
+    over = (a.double() - b.double()).abs() - (ulp + ref.pow(2).mean().sqrt() * 2.0 ** -16)
+    return float(over.max()) <= 0
 
 
 @pytest.mark.parametrize("k,n", [(1536, 256), (2048, 200), (1024, 40), (512, 8), (11008, 512), (3584, 1000)])
@@ -49,7 +54,7 @@ def test_every_split_against_fp64(cuda, reset_override, k, n):
                 set_split(waves, splits)
                 y = ops.gemv(x, wq, 6)
                 assert rel(y, ref) <= lim, (k, n, m, splits, waves)
-                assert ulps(y, base) <= 8, (k, n, m, splits, waves)
+                assert same_up_to_order(y, base, ref), (k, n, m, splits, waves)
                 assert torch.equal(ops.gemv(x, wq, 6), y)            # same bits on every call
 
 
@@ -64,7 +69,7 @@ def test_automatic_plan_splits_narrow_layers(cuda, reset_override):
         base = ops.gemv(x, wq, 6)
         _native.check(_native.lib().lowbit_set_launch_override(0, 0, 0))
         assert rel(auto, ref) <= bound(x, ref_w, ref), (k, n)
-        assert ulps(auto, base) <= 8, (k, n)
+        assert same_up_to_order(auto, base, ref), (k, n)
 
 
 @pytest.mark.parametrize("k,n", [(2048, 2048), (1536, 200)])
