@@ -40,8 +40,8 @@ CLIP_GRID = tuple(round(1.0 - 0.025 * i, 3) for i in range(11))       # referenc
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per GEMV launch of this workload, measured: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
 # `bench.py --pmc-workload` (20 eager steps), each scaled by what the counter reads for a 1 GiB elementwise copy in the
-# same run (FETCH x2.0, WRITE x1.0); 1.03x the algorithmic bytes. Re-measure when the kernel changes.
-TRAFFIC_PER_LAUNCH = 4713005
+# same run (FETCH x2.0, WRITE x1.0); 1.033x the algorithmic bytes. Re-measure when the kernel changes.
+TRAFFIC_PER_LAUNCH = 4724045
 MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
 
 
@@ -72,7 +72,9 @@ def parse():
     ap.add_argument("--no-detail", action="store_true", help="skip the per-shape timings")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny", "prefill"], default=None)
+    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles"], default=None,
+                    help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
+                         "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32")
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
@@ -359,7 +361,9 @@ def contract(a):
         # the timed graph holds only the M=1 GEMV kernel, so its average launch duration is elapsed / launches
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_PER_LAUNCH,
-                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false>",
+                     # one kernel template, three instances by layer: whole 16-row tiles (CS = 1: the 1.5B q/k/v/o
+                     # and both models' gate/up), tiles split over 2 workgroups (3B q/o, both downs) or 4 (3B k/v)
+                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false,CS>, CS = 1 / 2 / 4",
                      "kernel_avg_us": round(1000 * elapsed_ms / launches, 3), "launches": launches,
                      "bytes_per_launch_avg": step_bytes // len(projs)},
         "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,
@@ -424,6 +428,85 @@ def sweep_skinny(a):
             rows.append(r)
             print(json.dumps(r), flush=True)
         del pool, pool16
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
+# decode projections of the Qwen2.5-1.5B / 3B / 7B layers (K, N): q, k|v, o, gate / up, down and the merged q|k|v,
+# gate|up
+SWEEP_SHAPES = [(1536, 256), (1536, 1536), (1536, 2048), (1536, 8960), (1536, 17920), (8960, 1536), (2048, 256),
+                (2048, 2048), (2048, 2560), (2048, 11008), (2048, 22016), (11008, 2048), (3584, 512), (3584, 3584),
+                (3584, 4608), (3584, 18944), (18944, 3584)]
+
+
+def cloned_copies(torch, ops, k, n, gib=1.0):
+    """One absmax-quantized weight, cloned into >= gib GiB of copies (each call reads a cold copy)."""
+    w = torch.randn(n, k, device="cuda") * 0.02
+    p, s = ops.quantize_w4_gpu(w, GROUP)
+    base = ops.W4Weight(p, s, GROUP, ("mma",))
+    out = []
+    for _ in range(int(-(-gib * 2 ** 30 // w4_bytes(k, n)))):
+        c = ops.W4Weight.__new__(ops.W4Weight)
+        c.__dict__.update(base.__dict__)
+        c.packed_mma, c.scales = base.packed_mma.clone(), base.scales.clone()
+        out.append(c)
+    return out
+
+
+def sweep_gemv(a):
+    """M=1 GEMV (v6) per decode shape: graph-timed us per call of the automatic plan and of every tile split
+    CS (lowbit_set_launch_override k_splits: 1, 2, 4 workgroups per 16-row tile) x waves per workgroup."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in SWEEP_SHAPES:
+        cl = cloned_copies(torch, ops, k, n)
+        x = torch.randn(1, k, device="cuda").half()
+        t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 6), max(400, len(cl))), 2)
+        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+        r = {"K": k, "N": n, "auto_us": t(), "cs_waves_us": {}}
+        kc = k // 128
+        for cs in (1, 2, 4):
+            for waves in (1, 2, 4, 8, 16):
+                if kc % cs == 0 and waves <= kc // cs:
+                    _native.check(lib.lowbit_set_launch_override(waves, 0, cs))
+                    r["cs_waves_us"][f"{cs}x{waves}"] = t()
+        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+        rows.append(r)
+        print(json.dumps(r), flush=True)
+        del cl
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
+def sweep_tiles(a):
+    """MFMA GEMM (v5) per decode shape and M in 2..32: graph-timed us per call of the row-group kernel (automatic
+    shape), of one tile per workgroup with 2, 4 and 8 waves, and of the automatic choice (lowbit_set_gemm_kernel)."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in SWEEP_SHAPES:
+        cl = cloned_copies(torch, ops, k, n)
+        for m in (2, 4, 8, 16, 24, 32):
+            x = torch.randn(m, k, device="cuda").half()
+            t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5), max(300, len(cl))), 2)
+            r = {"K": k, "N": n, "M": m}
+            for name, kern, waves in (("rows", 1, 0), ("tiles_2", 2, 2), ("tiles_4", 2, 4), ("tiles_8", 2, 8),
+                                      ("auto", 0, 0)):
+                _native.check(lib.lowbit_set_gemm_kernel(kern))
+                _native.check(lib.lowbit_set_launch_override(waves, 0, 0))
+                r[name] = t()
+            _native.check(lib.lowbit_set_gemm_kernel(0))
+            _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+            rows.append(r)
+            print(json.dumps(r), flush=True)
+        del cl
         torch.cuda.empty_cache()
     if a.out:
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
@@ -681,6 +764,10 @@ def main():
         sweep_skinny(a)
     elif a.sweep == "prefill":
         sweep_prefill(a)
+    elif a.sweep == "gemv":
+        sweep_gemv(a)
+    elif a.sweep == "tiles":
+        sweep_tiles(a)
     elif a.e2e and a.decode_trace:
         decode_trace(a)
     elif a.e2e:

@@ -499,16 +499,18 @@ hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 }  // namespace
 
 // One tile per workgroup beats row groups, from an MI355X sweep (graph-timed, cold weights, M = 2..32 on the
-// Qwen2.5-1.5B/3B/7B projections), on the attention-sized layers: up to 288 tiles (N <= 4608) and K short enough that
-// every wave's own activation loads (4 KB per 1 KB of weights per 16 rows of M) stay cheap, KC * MT <= 32: 1.4-2.4x
-// (2048 x 2560, M = 16: 13.3 -> 5.6 us). Long K (8960 and up) or wide N keep row groups, which share the activations
-// through LDS.
-bool tiles_win(int MT, int ntiles, int KC) { return MT <= 2 && ntiles <= 288 && KC * MT <= 32; }
+// Qwen2.5-1.5B/3B/7B projections; bench.py --sweep tiles), on the attention-sized layers: up to 288 tiles (N <= 4608)
+// and K short enough that every wave's own activation loads (4 KB per 1 KB of weights per 16 rows of M) stay cheap,
+// KC * MT <= 56 (K <= 3584 up to M = 32): 1.1-2.4x (2048 x 2560, M = 16: 13.3 -> 5.6 us). Long K (8960 and up) or wide
+// N keep row groups, which share the activations through LDS.
+bool tiles_win(int MT, int ntiles, int KC) { return MT <= 2 && ntiles <= 288 && KC * MT <= 56; }
 
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
 // tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
-// N); K-groups per workgroup until about kGemmTargetWaves waves run; a 3-slot ring for M <= 16 with up to two K-groups,
-// else 2 slots.
+// N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
+// its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
+// split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
+// about kGemmTargetWaves waves run; a 3-slot ring for M <= 16 with up to two K-groups, else 2 slots.
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
   const GemvOverride o = gemv_override();
@@ -529,7 +531,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   if (o.splits > 0) {
     S = o.splits;
   } else if (part_bytes > 0) {
-    while (S < kMaxSplits && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 2 * S) S *= 2;
+    while (S < kMaxSplits && groups < 128 && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 2 * S) S *= 2;
   }
   S = std::min(S, std::max(1, KC));
   while (S > 1 && (size_t)S * M * N * sizeof(float) > part_bytes) --S;

@@ -151,11 +151,15 @@ def dequant(wq, layout=None):
 
 # version 0 (auto) picks by batch size and layer width. The structure is the reference's (lowbit/ops.py:137-160):
 # the v6 GEMV up to AUTO_GEMV_ROWS rows; the MFMA kernel (v5) up to AUTO_V5_ROWS rows on every layer and up to
-# AUTO_V5_WIDE_ROWS rows on layers with N >= AUTO_WIDE_N; dequantize + BLAS beyond. The constants come from an MI355X
-# sweep (graph-timed, weights cycled through >= 1 GiB, M in 1..64 on the Qwen2.5-3B/7B MLP shapes): the GEMV wins only
-# at M = 1; from M = 2 to 64 the MFMA kernel beats dequantize + hipBLASLt 2-6x and fp16 hipBLASLt on every shape, so
-# the width split of the reference's rule (which came from a T4) no longer matters.
+# AUTO_V5_WIDE_ROWS rows on layers with N >= AUTO_WIDE_N; dequantize + BLAS beyond. The constants come from MI355X
+# sweeps (graph-timed, weights cycled through >= 1 GiB, M in 1..64 on the Qwen2.5-1.5B/3B/7B projections): from M = 2
+# to 64 the MFMA kernel beats dequantize + hipBLASLt 2-6x and fp16 hipBLASLt on every shape, so the v5 width split of
+# the reference's rule (which came from a T4) no longer matters. The GEMV, which spends ALU per activation row, keeps
+# M = 2 and 3 on layers narrower than AUTO_GEMV_NARROW_N with K <= AUTO_GEMV_MAX_K (11008 x 2048, M = 2: 6.7 us vs
+# 11.5; q / o / k / v: 3.5-3.9 vs 3.8-4.6 us); wider layers and longer K go to v5 from M = 2 (2048 x 11008, M = 2: 7.0
+# vs 6.6 us). With AUTO_GEMV_NARROW_ROWS = AUTO_GEMV_ROWS the rule is exactly the reference's.
 AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 64, 64, 3072
+AUTO_GEMV_NARROW_ROWS, AUTO_GEMV_NARROW_N, AUTO_GEMV_MAX_K = 3, 8192, 16384
 # Beyond the MFMA kernel's rows (prefill), a weight on the mma layout with K >= AUTO_PREFILL_MIN_K goes to the
 # int4-direct prefill GEMM (prefill()), everything else to dequantize + BLAS. From the MI355X sweep at M = 128, 512,
 # 2048 on the Qwen2.5-3B / 7B projections: dequantize (4.4-4.8 TB/s) + hipBLASLt wins at K = 2048, 3584 and 11008;
@@ -172,7 +176,7 @@ def auto_version(m, wq):
     """The kernel linear() uses for m rows, or None for dequantize + BLAS. Weights without the mma layout (K or the
     group size not a multiple of 128) use v4 / v2 up to 8 rows."""
     if wq.packed_mma is not None:
-        if m <= AUTO_GEMV_ROWS:
+        if m <= AUTO_GEMV_ROWS or (m <= AUTO_GEMV_NARROW_ROWS and wq.n < AUTO_GEMV_NARROW_N and wq.k <= AUTO_GEMV_MAX_K):
             return 6
         return 5 if m <= (AUTO_V5_WIDE_ROWS if wq.n >= AUTO_WIDE_N else AUTO_V5_ROWS) else None
     if m <= 8:
@@ -198,7 +202,8 @@ def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or on long K the int4 prefill GEMM (prefill_path). version 0 =
     auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above.
     bias (fp16 [N], optional; not in the reference's signature): y = fp16(x W^T) + bias in fp16, the rounding of the
-    reference's linear() followed by `+ bias`; the v5 / v6 / prefill kernels add it in their store (no extra launch)."""
+    reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra
+    launch), multi-row v6 and dequantize + BLAS with a separate add."""
     m = x.shape[0]
     if m == 0:
         return x.new_empty(0, wq.n)
@@ -208,7 +213,9 @@ def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
         v = version if m <= (MAX_ROWS[5] if version == 5 else min(max_gemv_rows, MAX_ROWS[version])) else None
     else:
         raise ValueError(f"version must be 0 (auto) or one of {sorted(MAX_ROWS)}")
-    if bias is not None and v in (5, 6):
+    # the fused entry runs the GEMV for one row and the MFMA kernel for more: fuse the bias where that is the kernel
+    # the unbiased call would run, so linear(bias=b) stays linear() + b bit for bit
+    if bias is not None and (v == 5 or (v == 6 and m == 1)):
         return ext().w4_linear_fused(x.contiguous(), wq.packed_mma, wq.scales, wq.group, _native.EPI_BIAS, bias)
     if v is not None:
         y = gemv(x, wq, v)

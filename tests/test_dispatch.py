@@ -25,20 +25,25 @@ def calls(monkeypatch):
 
 def _rule_cases():
     g, v5, v5w, wide = ops.AUTO_GEMV_ROWS, ops.AUTO_V5_ROWS, ops.AUTO_V5_WIDE_ROWS, ops.AUTO_WIDE_N
+    gn, gwide, kmax = ops.AUTO_GEMV_NARROW_ROWS, ops.AUTO_GEMV_NARROW_N, ops.AUTO_GEMV_MAX_K
     narrow, wide_n = max(256, wide // 2), wide
-    return [(1, narrow, 6), (g, narrow, 6), (g + 1, narrow, 5), (v5, narrow, 5), (v5 + 1, narrow, "dequant"),
-            (v5 + 1, wide_n, 5 if v5w > v5 else "dequant"), (v5w, wide_n, 5), (v5w + 1, wide_n, "dequant")]
+    return [(1, narrow, 256, 6), (g, narrow, 256, 6), (gn, narrow, 256, 6), (gn + 1, narrow, 256, 5),
+            (g + 1, gwide, 256, 5), (gn, gwide - 16, 256, 6), (g + 1, narrow, kmax + 128, 5), (gn, narrow, kmax, 6),
+            (1, gwide, kmax + 128, 6), (v5, narrow, 256, 5), (v5 + 1, narrow, 256, "dequant"),
+            (v5 + 1, wide_n, 256, 5 if v5w > v5 else "dequant"), (v5w, wide_n, 256, 5),
+            (v5w + 1, wide_n, 256, "dequant")]
 
 
-@pytest.mark.parametrize("m,n,want", _rule_cases())
-def test_auto_rule_on_the_mma_layout(calls, m, n, want):
-    ops.linear(torch.zeros(m, 256), weight(n))
+@pytest.mark.parametrize("m,n,k,want", _rule_cases())
+def test_auto_rule_on_the_mma_layout(calls, m, n, k, want):
+    ops.linear(torch.zeros(m, k), weight(n, k))
     assert calls == [want]
 
 
 def test_reference_table_with_the_t4_constants(calls, monkeypatch):
     """The rule's structure reproduces the reference's own table when given the reference's (T4) constants."""
-    for name, value in (("AUTO_GEMV_ROWS", 1), ("AUTO_V5_ROWS", 32), ("AUTO_V5_WIDE_ROWS", 64), ("AUTO_WIDE_N", 3072)):
+    for name, value in (("AUTO_GEMV_ROWS", 1), ("AUTO_V5_ROWS", 32), ("AUTO_V5_WIDE_ROWS", 64), ("AUTO_WIDE_N", 3072),
+                        ("AUTO_GEMV_NARROW_ROWS", 1)):
         monkeypatch.setattr(ops, name, value)
     for m, n, want in [(1, 1024, 6), (2, 1024, 5), (32, 1024, 5), (33, 1024, "dequant"), (33, 4096, 5), (64, 4096, 5),
                        (65, 4096, "dequant")]:
