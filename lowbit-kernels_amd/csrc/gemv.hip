@@ -220,9 +220,9 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[i][m] = 0.f;
 
-  // this wave's wave-loads are c_j = wave + j * nwaves, j < nj (wave-load c holds chunks CS c .. CS c + CS - 1). Full
-  // groups of D refill their slot D wave-loads ahead (past the end the refill reads zeros); the last partial group
-  // drains the ring without refills.
+  // this wave's wave-loads are c_j = wave + j * nwaves, j < nj (wave-load c holds chunks CS c .. CS c + CS - 1). Groups
+  // of D followed by another refill their slot D wave-loads ahead (a refill past the end reads zeros and is never
+  // consumed); the last group, up to D wave-loads, drains the ring without refills.
   const int nj = (KC / CS - wave + nwaves - 1) / nwaves;
   const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
   auto consume = [&](const u32x4 (&slot)[R], int cw) {
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
   };
   int j0 = 0;
-  for (; j0 + D <= nj; j0 += D) {
+  for (; j0 + D < nj; j0 += D) {                            // a later group follows: refill behind each consume
 #pragma unroll
     for (int d = 0; d < D; ++d) {
       const int c = wave + (j0 + d) * nwaves;
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
   }
 #pragma unroll
-  for (int d = 0; d < D - 1; ++d)
+  for (int d = 0; d < D; ++d)                                // the last group, up to D wave-loads, without refills
     if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
 
   // RoPE epilogue (M = 1): rows n (dim d of a head) and n + 8 (dim d + 64) -> bias, RoPE, q_out or the caches
