@@ -224,6 +224,11 @@ class FusedDecoder:
         with torch.cuda.graph(self.graph):
             self.logits = self.f(self.tokens, self.positions)
             self.next_token = self.logits[-1].argmax(-1)
+            if self.chunk == 1:
+                # greedy feedback for the next replay: the argmax becomes the input, one position on. step() sets both
+                # buffers before each replay, so feeding given tokens is unaffected; greedy() runs replays back to back
+                self.tokens.copy_(self.next_token.view(1))
+                self.positions.add_(1)
         return self
 
     def step(self, tokens):
@@ -239,9 +244,14 @@ class FusedDecoder:
     def greedy(self, first, n):
         if self.chunk != 1:
             raise ValueError("greedy decoding feeds one token per step")
+        if self.pos + n - 1 > self.f.max_len:
+            raise ValueError("the cache is full")
         out = torch.empty(n, dtype=torch.long, device=self.tokens.device)
         out[0] = first
-        for i in range(1, n):
-            self.step(out[i - 1])
+        self.tokens.copy_(out[:1])
+        self.positions.fill_(self.pos)
+        for i in range(1, n):                               # the graph feeds its argmax back (capture)
+            self.graph.replay()
+            self.pos += 1
             out[i] = self.next_token
         return out

@@ -212,6 +212,30 @@ def tiny_models():
     return decode.random_model("tiny", seed=21)
 
 
+def test_fused_greedy_feeds_its_argmax_back_in_the_graph(cuda, tiny_models):
+    """FusedDecoder.greedy (replays back to back, the graph writing its argmax into the next input and advancing the
+    position) gives the tokens of stepping the same graph with the argmax fed by hand, for fp16 and int4
+    projections; step() afterwards still feeds the given token."""
+    m = tiny_models
+    prompt = torch.randint(0, 1024, (1, 30), generator=torch.Generator(device="cuda").manual_seed(9), device="cuda")
+    for quant in ("fp16", "int4"):
+        f = fused.FusedQwen2(m, 30 + 40, quant=quant)
+        dec = fused.FusedDecoder(f, chunk=1)
+        first = dec.prefill(prompt).argmax(-1)
+        dec.capture()
+        toks = dec.greedy(first, 24)
+        ref = fused.FusedDecoder(f, chunk=1)
+        nxt = ref.prefill(prompt).argmax(-1)
+        ref.capture()
+        by_hand = [int(nxt)]
+        for _ in range(23):
+            by_hand.append(int(ref.step(torch.tensor([by_hand[-1]], device="cuda"))[-1].argmax(-1)))
+        assert toks.tolist() == by_hand, quant
+        assert dec.pos == ref.pos
+        logits = dec.step(torch.tensor([by_hand[-1]], device="cuda")).clone()
+        assert torch.equal(logits, ref.step(torch.tensor([by_hand[-1]], device="cuda"))), quant
+
+
 def test_fused_qwen2_matches_transformers(cuda, tiny_models):
     m = tiny_models
     gen = torch.Generator(device="cuda").manual_seed(5)
