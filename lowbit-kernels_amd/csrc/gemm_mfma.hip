@@ -297,9 +297,10 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   }
 }
 
-// gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 32 on layers with few tiles.
-// The row-group kernel above must split K over workgroups there (and pay an agent-scope release per workgroup to add
-// the partials); here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
+// gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 32 on attention-sized layers
+// (few tiles, short K; the selection rule is tiles_win below). The row-group kernel above stages activations for 64
+// rows with a barrier per chunk and, on narrow layers, splits K over workgroups that each pay an agent-scope release to
+// add the partials; here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
 // the end, so no workgroup waits for another. Each wave loads, next to its weight piece, the activation piece its B
 // fragments need (lane l: 64 contiguous bytes, x row 16 mt + l % 16, k = 128 c + 32 (l / 16) + [0, 32)) straight into
 // registers: no staging buffer and no barrier inside the K loop. Lane l's weight piece is row l % 16, quarter l / 16
