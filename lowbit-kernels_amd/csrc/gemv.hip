@@ -62,6 +62,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   static_assert(CS == 1 || (R == 1 && (CS == 2 || CS == 4)), "a tile splits over 2 or 4 workgroups, one tile each");
   constexpr int RS = 16 / CS;                               // rows of a tile one workgroup owns
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
+  constexpr int kScaleLoads = 4;                            // scales per thread requested before the ring
   // norm_w (M = 1 with x in LDS only; the launcher then gives every block of x a thread): the projection's input is
   // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
   const bool norm = kFused && kLdsX && M == 1 && norm_w != nullptr;   // kFused: epilogue / norm code compiled in
@@ -78,8 +79,9 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
   const int t0 = (CS == 1 ? (int)blockIdx.x : (int)blockIdx.x / CS) * R;
   // rows of this workgroup (none for the second half or quarters of a tile cut short by N: such a workgroup reads
-  // only zeros and stores nothing)
-  const int n0 = 16 * t0 + RS * sub, nrows = max(0, min(RS * R, N - n0));
+  // only zeros and stores nothing). The clamp is computed per lane (v_med3); readfirstlane keeps the scale buffer
+  // resource built from it in scalar registers, where a per-lane value would make every scale load a waterfall loop.
+  const int n0 = 16 * t0 + RS * sub, nrows = __builtin_amdgcn_readfirstlane(max(0, min(RS * R, N - n0)));
   // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16
   f16* lds_x = reinterpret_cast<f16*>(smem);
   float* lds_xs = reinterpret_cast<float*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
@@ -111,11 +113,13 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       }
     }
   }
-  uint16_t sst[2];
+  // up to kScaleLoads scales per thread, all in flight before the weights (loads complete in issue order, so a
+  // thread's later ones, loaded while staging, would each wait for the whole ring)
+  uint16_t sst[kScaleLoads];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < kScaleLoads; ++u) {
     const int i = (int)threadIdx.x + u * (int)blockDim.x;
-    if (i < ns) sst[u] = buffer_load2(sr, 2 * i);
+    if (i < ns) sst[u] = buffer_load2_nt(sr, 2 * i);
   }
 
   // 2. the weight ring
@@ -206,12 +210,12 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
   }
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < kScaleLoads; ++u) {
     const int i = (int)threadIdx.x + u * (int)blockDim.x;
     if (i < ns) reinterpret_cast<uint16_t*>(lds_s)[i] = sst[u];
   }
-  for (int i = (int)threadIdx.x + 2 * (int)blockDim.x; i < ns; i += blockDim.x)
-    reinterpret_cast<uint16_t*>(lds_s)[i] = buffer_load2(sr, 2 * i);
+  for (int i = (int)threadIdx.x + kScaleLoads * (int)blockDim.x; i < ns; i += blockDim.x)   // > 4 per thread only
+    reinterpret_cast<uint16_t*>(lds_s)[i] = buffer_load2_nt(sr, 2 * i);
   __syncthreads();
 
   float acc[R][M];
