@@ -260,7 +260,9 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
                                                        f16* __restrict__ y, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave through readfirstlane: the row buffer resource below is then known uniform and stays in scalar registers
+  // (from a per-lane value every weight load becomes a waterfall loop)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kp = K >> 3;                                     // 16-byte pieces per row
   for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
   __syncthreads();
