@@ -513,9 +513,10 @@ def sweep_tiles(a):
 
 
 def sweep_prefill(a):
-    """Prefill, M in {128, 512, 2048} on the Qwen2.5-3B layer (merged q|k|v and gate|up, o, down) and the 7B MLP
-    projections: us/call of dequantize + hipBLASLt, fp16 hipBLASLt, the int4 prefill GEMM (automatic launch plan) and
-    linear() (auto route), each a graph cycling >= 1 GiB of int4 copies (fp16: >= 1 GiB of fp16 copies)."""
+    """Prefill, M in {128, 256, 512, 2048} on the Qwen2.5-3B layer (merged q|k|v and gate|up, o, down) and the 7B MLP
+    projections: us/call of dequantize + hipBLASLt, fp16 hipBLASLt, the int4 prefill GEMM (automatic launch plan), the
+    v5 MFMA kernel in 64-row slices (ops.gemm_chunked, M <= 512) and linear() (auto route), each a graph cycling
+    >= 1 GiB of int4 copies (fp16: >= 1 GiB of fp16 copies)."""
     import torch
     from lowbit import ops
     torch.cuda.set_device(0)
@@ -526,7 +527,7 @@ def sweep_prefill(a):
         projs = [(name, k, n)]
         pool, pool16, _, copies = build_pool(torch, ops, projs, fp16=True, seed=k + n)
         e = ops.ext()
-        for m in (128, 512, 2048):
+        for m in (128, 256, 512, 2048):
             x = torch.randn(m, k, device="cuda").half()
             r = {"shape": name, "K": k, "N": n, "M": m, "copies": copies}
             it = max(40, copies)
@@ -535,6 +536,8 @@ def sweep_prefill(a):
             r["fp16_blas_us"] = round(graph_time_us(torch, lambda i: torch.nn.functional.linear(
                 x, pool16[i % copies][name]), it), 2)
             r["int4_prefill_us"] = round(graph_time_us(torch, lambda i: ops.prefill(x, pool[i % copies][name]), it), 2)
+            r["v5_chunked_us"] = (round(graph_time_us(torch, lambda i: ops.gemm_chunked(x, pool[i % copies][name]), it), 2)
+                                  if m <= 512 else None)
             r["linear_us"] = round(graph_time_us(torch, lambda i: ops.linear(x, pool[i % copies][name]), it), 2)
             r["linear_path"] = "prefill" if ops.prefill_path(m, pool[0][name]) else "dequant+blas"
             r["int4_prefill_tflops"] = round(2 * m * n * k / (r["int4_prefill_us"] * 1e-6) / 1e12, 1)

@@ -160,11 +160,15 @@ def dequant(wq, layout=None):
 # vs 6.6 us). With AUTO_GEMV_NARROW_ROWS = AUTO_GEMV_ROWS the rule is exactly the reference's.
 AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 64, 64, 3072
 AUTO_GEMV_NARROW_ROWS, AUTO_GEMV_NARROW_N, AUTO_GEMV_MAX_K = 3, 8192, 16384
-# Beyond the MFMA kernel's rows (prefill), a weight on the mma layout with K >= AUTO_PREFILL_MIN_K goes to the
-# int4-direct prefill GEMM (prefill()), everything else to dequantize + BLAS. From the MI355X sweep at M = 128, 512,
-# 2048 on the Qwen2.5-3B / 7B projections: dequantize (4.4-4.8 TB/s) + hipBLASLt wins at K = 2048, 3584 and 11008;
-# the int4 kernel wins only on the long-K 7B down projection (K = 18944: 1.06x, 1.56x, 1.13x).
+# Beyond the MFMA kernel's rows (prefill), a weight on the mma layout with K >= AUTO_PREFILL_MIN_K, or with
+# N >= AUTO_PREFILL_WIDE_N for at most AUTO_PREFILL_WIDE_ROWS rows, goes to the int4-direct prefill GEMM (prefill()),
+# everything else to dequantize + BLAS. From the MI355X sweep at M = 128, 256, 512, 2048 on the Qwen2.5-3B / 7B
+# projections: dequantize (4.4-4.8 TB/s) + hipBLASLt wins at K = 2048, 3584 and 11008 except on the wide gate|up
+# layers up to 256 rows (3B merged 2048 x 22016: 43.5 vs 48.2 us at M = 128, 49.3 vs 55.9 at 256; 7B 3584 x 18944:
+# 65.1 vs 66.5, 74.1 vs 80.5), where writing the fp16 copy costs more than the int4 kernel's lower MFMA rate; the
+# int4 kernel always wins on the long-K 7B down projection (K = 18944: 1.21x, 1.26x, 1.54x, 1.09x).
 AUTO_PREFILL_MIN_K = 16384
+AUTO_PREFILL_WIDE_N, AUTO_PREFILL_WIDE_ROWS = 16384, 256
 
 
 def gemm_chunked(x, wq, chunk=64):
@@ -194,13 +198,16 @@ def prefill(x, wq):
 
 def prefill_path(m, wq):
     """True when linear() sends m rows to the int4 prefill GEMM rather than dequantize + BLAS (auto routing only)."""
-    return auto_version(m, wq) is None and wq.packed_mma is not None and wq.k >= AUTO_PREFILL_MIN_K
+    if auto_version(m, wq) is not None or wq.packed_mma is None:
+        return False
+    return wq.k >= AUTO_PREFILL_MIN_K or (wq.n >= AUTO_PREFILL_WIDE_N and m <= AUTO_PREFILL_WIDE_ROWS)
 
 
 def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     """Decode (few rows): an INT4 kernel (v6 GEMV for one row, v5 MFMA beyond). Prefill (many rows): dequantize, then
-    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or on long K the int4 prefill GEMM (prefill_path). version 0 =
-    auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5: 64), and dequantize + BLAS above.
+    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM on long K and on wide N up to 256
+    rows (prefill_path). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5:
+    64), and dequantize + BLAS above.
     bias (fp16 [N], optional; not in the reference's signature): y = fp16(x W^T) + bias in fp16, the rounding of the
     reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra
     launch), multi-row v6 and dequantize + BLAS with a separate add."""

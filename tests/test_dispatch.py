@@ -65,6 +65,19 @@ def test_prefill_rule(calls):
         assert calls == [want], (m, k, layouts, version)
 
 
+def test_prefill_rule_for_wide_layers(calls):
+    """Short-K weights with N >= AUTO_PREFILL_WIDE_N take the int4 prefill GEMM up to AUTO_PREFILL_WIDE_ROWS rows,
+    dequantize + BLAS beyond; narrower N never does."""
+    wide, rows, v5 = ops.AUTO_PREFILL_WIDE_N, ops.AUTO_PREFILL_WIDE_ROWS, ops.AUTO_V5_WIDE_ROWS
+    k = 2048
+    assert k < ops.AUTO_PREFILL_MIN_K
+    for m, n, want in [(v5 + 1, wide, "prefill"), (rows, wide, "prefill"), (rows + 1, wide, "dequant"),
+                       (rows, wide - 16, "dequant"), (v5, wide, 5), (rows, 2 * wide, "prefill")]:
+        calls.clear()
+        ops.linear(torch.zeros(m, k), weight(n, k))
+        assert calls == [want], (m, n)
+
+
 @pytest.mark.parametrize("layouts,m,want", [(("canonical", "v3"), 1, 4), (("canonical", "v3"), 8, 4),
                                             (("canonical",), 3, 2), (("canonical", "v3"), 9, "dequant")])
 def test_auto_rule_without_the_mma_layout(calls, layouts, m, want):
