@@ -58,6 +58,11 @@ constexpr int kQuadSwap2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
 constexpr int kRowHalfMirror = 0x141;  // lane ^ 7 inside 8 lanes
 constexpr int kRowMirror = 0x140;      // lane ^ 15 inside 16 lanes
 
+template <int kV>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {   // value of lane kV of each quad
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kV | (kV << 2) | (kV << 4) | (kV << 6), 0xF, 0xF, false);
+}
+
 // sum over the 4 lanes of a quad; every lane of the quad gets the total
 __device__ __forceinline__ float quad_sum(float v) {
   v += dpp<kQuadSwap1>(v);

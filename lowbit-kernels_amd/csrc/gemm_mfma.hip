@@ -39,11 +39,6 @@ constexpr int kW = 4;              // waves per workgroup
 constexpr int kXPitch = 272;       // bytes per staged activation row (256 + 16: conflict-free 16-byte LDS reads)
 constexpr float kTwo24 = 16777216.0f;
 
-template <int kV>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {   // value of lane kV of each quad
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kV | (kV << 2) | (kV << 4) | (kV << 6), 0xF, 0xF, false);
-}
-
 }  // namespace
 
 template <int MT, int RW, int D, int KS>
