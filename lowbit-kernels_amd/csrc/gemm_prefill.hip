@@ -9,7 +9,8 @@
 //   B (32 k x 16 activation rows): x[m0 + 16 mt + r][128 c + 32 q + 8 s + 0..7], 16 bytes from LDS.
 //   D: lane l holds y[m0 + 16 mt + r][16 t + 4 q + v], v = 0..3.
 //
-// Workgroup: 4 waves, each owning 4 16-row tiles (256 weight rows per workgroup), against 16 MT activation rows.
+// Workgroup: 4 waves, each owning PT 16-row tiles (64 PT weight rows per workgroup; PT = 4, or 2 or 1 when the grid
+// would leave CUs idle), against 16 MT activation rows.
 // Every wave decodes only its own rows, so no weight is decoded twice; the activation chunk is loaded once per
 // workgroup (16 bytes per thread and row piece) and shared through LDS, double buffered with one barrier per 128-k
 // chunk. LDS rows are 256 bytes with the 16-byte column blocks XOR-swizzled by the row (block b of row m at
@@ -31,19 +32,18 @@ namespace lowbit {
 
 namespace {
 
-constexpr int kPT = 4;                    // 16-row tiles per wave
 
 __device__ __forceinline__ int swz(int row, int blk) { return row * 16 + (blk ^ (row & 15)); }   // 16-byte slot
 
 }  // namespace
 
-template <int MT, int D, int NW, int XL>
+template <int MT, int D, int NW, int XL, int PT>
 __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                     const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                     int S, int MG, int items, uint32_t* __restrict__ ctr,
                                                     float* __restrict__ part, Epilogue epi) {
   constexpr int kXBuf = 16 * MT * 256;                      // one staged chunk of x
-  constexpr int kRows = 64 * NW;                            // weight rows per workgroup
+  constexpr int kRows = 16 * PT * NW;                       // weight rows per workgroup
   args_in_sgprs(x, w, s, y, M, N, K, G, S, MG, items, ctr, part, epi.aux);
   constexpr int kThreads = 64 * NW;
   constexpr int XP = 16 * MT * 16 / kThreads;               // 16-byte x pieces per thread and chunk
@@ -65,11 +65,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   const int nsteps = ce - cb;
   const size_t tile_bytes = (size_t)8 * K;
 
-  __amdgpu_buffer_rsrc_t wr[kPT];
-  int woff[kPT], wstep[kPT], soff[kPT];
+  __amdgpu_buffer_rsrc_t wr[PT];
+  int woff[PT], wstep[PT], soff[PT];
 #pragma unroll
-  for (int i = 0; i < kPT; ++i) {
-    const int t = n0 / 16 + kPT * wave + i;
+  for (int i = 0; i < PT; ++i) {
+    const int t = n0 / 16 + PT * wave + i;
     const int tc = min(t, ntiles - 1);
     const int rows = t < ntiles ? min(16, N - 16 * t) : 0;
     wr[i] = make_rsrc(w + tc * tile_bytes, (uint32_t)(rows * (K / 2)));
@@ -87,14 +87,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
     xslot[u] = 16 * swz(pc >> 4, pc & 15);
   }
 
-  u32x4 rw[D][kPT], rx[XL][XP];
-  uint32_t rs[D][kPT];
+  u32x4 rw[D][PT], rx[XL][XP];
+  uint32_t rs[D][PT];
   const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
   auto issue_w = [&](int d, int c) {
     const bool live = c < ce;
     const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
 #pragma unroll
-    for (int i = 0; i < kPT; ++i) {
+    for (int i = 0; i < PT; ++i) {
       rw[d][i] = buffer_load16(wr[i], live ? woff[i] + c * wstep[i] : kOutOfRange);   // re-read by other m-groups
       rs[d][i] = buffer_load2(sr, live ? soff[i] + 2 * g : kOutOfRange);
     }
@@ -108,9 +108,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
     for (int u = 0; u < XP; ++u) *reinterpret_cast<u32x4*>(smem + b * kXBuf + xslot[u]) = rx[e][u];
   };
 
-  f32x4 acc[kPT][MT];
+  f32x4 acc[PT][MT];
 #pragma unroll
-  for (int i = 0; i < kPT; ++i)
+  for (int i = 0; i < PT; ++i)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -119,9 +119,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   // one chunk: the 16 A fragments (4 tiles x 4 k-steps) are decoded first; then per activation tile its 4 B
   // fragments are read and 16 MFMAs issued, so at most two tiles' B fragments are live
   auto consume = [&](int d, int b) {
-    f16x8 a[kPT][4];
+    f16x8 a[PT][4];
 #pragma unroll
-    for (int i = 0; i < kPT; ++i) {
+    for (int i = 0; i < PT; ++i) {
       const f16 sv = __builtin_bit_cast(f16, (uint16_t)rs[d][i]);
       const f16x2 sc = {sv, sv};
 #pragma unroll
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
 #pragma unroll
       for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int i = 0; i < kPT; ++i) acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][st], bx[st], acc[i][mt], 0, 0, 0);
+        for (int i = 0; i < PT; ++i) acc[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i][st], bx[st], acc[i][mt], 0, 0, 0);
     }
   };
 
@@ -202,10 +202,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   };
   if (S == 1) {
 #pragma unroll
-    for (int i = 0; i < kPT; ++i)
+    for (int i = 0; i < PT; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int m = m0 + 16 * mt + r, n = n0 + 16 * (kPT * wave + i) + 4 * q;
+        const int m = m0 + 16 * mt + r, n = n0 + 16 * (PT * wave + i) + 4 * q;
         const f32x4 v = acc[i][mt];
         if (epi.mode == kEpiSiluMul) {                      // up rows 8 + 4 q + v sit 32 lanes on (q + 2)
           const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
@@ -219,10 +219,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   }
   float* mine = part + (size_t)sp * M * N;                  // [S][M][N] fp32
 #pragma unroll
-  for (int i = 0; i < kPT; ++i)
+  for (int i = 0; i < PT; ++i)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = m0 + 16 * mt + r, n = n0 + 16 * (kPT * wave + i) + 4 * q;
+      const int m = m0 + 16 * mt + r, n = n0 + 16 * (PT * wave + i) + 4 * q;
       if (m >= M || n >= N) continue;
       float* dst = mine + (size_t)m * N + n;
       if (vec) {
@@ -269,13 +269,13 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
 
 namespace {
 
-template <int MT, int D, int NW, int XL>
+template <int MT, int D, int NW, int XL, int PT = 4>
 hipError_t launch_prefill(const GemvArgs& a, const PrefillPlan& p, uint32_t* ctr, float* part) {
   if constexpr (!prefill_fits(MT, D, NW, XL)) {
     return hipErrorInvalidConfiguration;                    // never planned
   } else {
   const size_t shmem = (size_t)2 * 16 * MT * 256;
-  auto kern = gemm_prefill<MT, D, NW, XL>;
+  auto kern = gemm_prefill<MT, D, NW, XL, PT>;
   if (shmem > 65536) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
@@ -288,18 +288,23 @@ hipError_t launch_prefill(const GemvArgs& a, const PrefillPlan& p, uint32_t* ctr
 
 template <int MT, int NW>
 hipError_t dispatch_prefill_ring(const GemvArgs& a, const PrefillPlan& p, uint32_t* ctr, float* part) {
+  if constexpr (MT == 4 && NW == 4) {                       // fewer tiles per wave: the default shape only
+    if (p.D == 2 && p.XL == 1 && p.PT == 1) return launch_prefill<4, 2, 4, 1, 1>(a, p, ctr, part);
+    if (p.D == 2 && p.XL == 1 && p.PT == 2) return launch_prefill<4, 2, 4, 1, 2>(a, p, ctr, part);
+  }
   if (p.D == 3) return launch_prefill<MT, 3, NW, 1>(a, p, ctr, part);
   return p.XL == 2 ? launch_prefill<MT, 2, NW, 2>(a, p, ctr, part) : launch_prefill<MT, 2, NW, 1>(a, p, ctr, part);
 }
 
 }  // namespace
 
-// Launch shape from an MI355X sweep (graph-timed, M = 128 / 512 / 2048 on the Qwen2.5-3B and 7B projections): 64
-// activation rows x 4 waves with a 2-deep weight ring (2 workgroups per CU; deeper rings or the x lookahead cost the
-// second wave per SIMD and lose); K split into the largest power of two that keeps >= 16 chunks per split and at most
-// two rounds of kPrefillTargetGroups workgroups, within the workspace and the counters. The tuning override selects
-// (waves_per_group: 1 = MT 4 / 4 waves, 2 = MT 4 / 8 waves, 4 = MT 8 / 4 waves, 8 = MT 8 / 8 waves; ring: 2 or 3 =
-// weight chunks in flight, 4 = two in flight with a two-chunk x lookahead).
+// Launch shape from an MI355X sweep (graph-timed, M = 128 / 256 / 512 / 2048 on the Qwen2.5-3B and 7B projections):
+// 64 activation rows x 4 waves with a 2-deep weight ring (2 workgroups per CU; deeper rings or the x lookahead cost
+// the second wave per SIMD and lose), 4, 2 or 1 weight tiles per wave (below); K split into the largest power of two
+// that keeps >= 16 chunks per split and at most two rounds of kPrefillTargetGroups workgroups, within the workspace
+// and the counters. The tuning override selects (waves_per_group: 1 = MT 4 / 4 waves, 2 = MT 4 / 8 waves, 4 = MT 8 /
+// 4 waves, 8 = MT 8 / 8 waves; ring: 2 or 3 = weight chunks in flight, 4 = two in flight with a two-chunk x lookahead),
+// always with 4 tiles per wave.
 PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes) {
   PrefillPlan p;
   const GemvOverride o = gemv_override();
@@ -315,9 +320,16 @@ PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes) {
   p.XL = o.ring == 4 ? 2 : 1;
   if (!prefill_fits(p.MT, p.D, p.NW, p.XL)) p.NW = 4;      // 8 waves: 256 registers per wave, D = 2 and MT = 4 only
   if (!prefill_fits(p.MT, p.D, p.NW, p.XL)) p.D = 2;
-  const int NG = (N + 64 * p.NW - 1) / (64 * p.NW);
   p.MG = (M + 16 * p.MT - 1) / (16 * p.MT);
-  const long tiles = (long)NG * p.MG;
+  // fewer 16-row tiles per wave (default shape only) while the grid holds less than two workgroups per CU. A wave's
+  // activation bytes per chunk stay the same while its weight bytes shrink (x : w = 4 : PT), so past 4 activation
+  // tiles a long K (>= 128 chunks) splits across workgroups instead (measured: 7B down, M = 512, 130 us at 4 tiles
+  // and 2 splits vs 142 at 1 tile; M = 2048, 351 vs 451; at M <= 256 and on K <= 11008 the thin tiles win up to 2.9x)
+  auto groups = [&](int pt) { return (long)((N + 16 * pt * p.NW - 1) / (16 * pt * p.NW)) * p.MG; };
+  p.PT = 4;
+  if (o.waves == 0 && o.ring == 0 && (KC < 128 || p.MG <= 4))
+    while (p.PT > 1 && groups(p.PT) < 2 * kPrefillTargetGroups) p.PT /= 2;
+  const long tiles = groups(p.PT);
   const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
   int S = 1;
   if (o.splits > 0) {

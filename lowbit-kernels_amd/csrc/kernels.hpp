@@ -59,8 +59,9 @@ struct PrefillPlan {
   int S = 1;        // workgroups splitting K per tile
   int MG = 1;       // activation-row groups
   int items = 1;    // workgroups: tiles x S
-  int NW = 4;       // waves per workgroup, 64 weight rows each
+  int NW = 4;       // waves per workgroup, 16 PT weight rows each
   int XL = 1;       // chunks of x in flight
+  int PT = 4;       // 16-row weight tiles per wave
 };
 
 // process-wide launch-shape override for tuning sweeps (lowbit_set_launch_override); 0 = automatic

@@ -58,8 +58,7 @@ class _W4:
         wq = self.wq
         if x.shape[0] <= 64:
             return ops.ext().w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out, norm)
-        if ops.prefill_path(x.shape[0], wq):                 # long K, or wide N up to 256 rows: the int4
-            # prefill GEMM, epilogue fused
+        if ops.prefill_path(x.shape[0], wq):                 # the int4 prefill GEMM, epilogue fused
             return ops.ext().w4_gemm_prefill(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out)
         w = ops.dequant(wq)                                  # prefill: dequantize + hipBLASLt, epilogue in torch
         return _torch_epilogue(x, w, epilogue, aux, out)

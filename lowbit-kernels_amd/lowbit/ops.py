@@ -160,15 +160,16 @@ def dequant(wq, layout=None):
 # vs 6.6 us). With AUTO_GEMV_NARROW_ROWS = AUTO_GEMV_ROWS the rule is exactly the reference's.
 AUTO_GEMV_ROWS, AUTO_V5_ROWS, AUTO_V5_WIDE_ROWS, AUTO_WIDE_N = 1, 64, 64, 3072
 AUTO_GEMV_NARROW_ROWS, AUTO_GEMV_NARROW_N, AUTO_GEMV_MAX_K = 3, 8192, 16384
-# Beyond the MFMA kernel's rows (prefill), a weight on the mma layout with K >= AUTO_PREFILL_MIN_K, or with
-# N >= AUTO_PREFILL_WIDE_N for at most AUTO_PREFILL_WIDE_ROWS rows, goes to the int4-direct prefill GEMM (prefill()),
-# everything else to dequantize + BLAS. From the MI355X sweep at M = 128, 256, 512, 2048 on the Qwen2.5-3B / 7B
-# projections: dequantize (4.4-4.8 TB/s) + hipBLASLt wins at K = 2048, 3584 and 11008 except on the wide gate|up
-# layers up to 256 rows (3B merged 2048 x 22016: 43.5 vs 48.2 us at M = 128, 49.3 vs 55.9 at 256; 7B 3584 x 18944:
-# 65.1 vs 66.5, 74.1 vs 80.5), where writing the fp16 copy costs more than the int4 kernel's lower MFMA rate; the
-# int4 kernel always wins on the long-K 7B down projection (K = 18944: 1.21x, 1.26x, 1.54x, 1.09x).
-AUTO_PREFILL_MIN_K = 16384
-AUTO_PREFILL_WIDE_N, AUTO_PREFILL_WIDE_ROWS = 16384, 256
+# Beyond the MFMA kernel's rows (prefill), a weight on the mma layout goes to the int4-direct prefill GEMM (prefill())
+# when K >= AUTO_PREFILL_MIN_K, when M <= AUTO_PREFILL_ROWS, or when M <= AUTO_PREFILL_NARROW_ROWS on a small layer
+# (N and K <= AUTO_PREFILL_NARROW); everything else dequantizes (4.4-4.8 TB/s) and calls BLAS. From the MI355X sweep at
+# M = 128, 256, 512, 2048 on the Qwen2.5-3B / 7B projections (int4 vs dequantize + hipBLASLt, us): the attention-sized
+# 3B layers up to 512 rows (q|k|v 14.3 vs 21.4 at M = 128, 18.4 vs 25.0 at 512; o 14.3 vs 21.9 at 512), every layer up
+# to 256 rows (3B merged gate|up 27.3 vs 46.4 at 128, 39.7 vs 56.7 at 256; 3B down 32.3 vs 37.4 at 128, 47.0 vs 47.4
+# at 256) and the long-K 7B down at every M (60 vs 109 at 128, 130 vs 202 at 512); dequantize + hipBLASLt keeps the
+# wide and long layers from 512 rows (3B gate|up at 512: 77 vs 89, 3B down 58 vs 67) and the small ones at 2048.
+AUTO_PREFILL_MIN_K, AUTO_PREFILL_ROWS = 16384, 256
+AUTO_PREFILL_NARROW, AUTO_PREFILL_NARROW_ROWS = 4096, 512
 
 
 def gemm_chunked(x, wq, chunk=64):
@@ -200,13 +201,14 @@ def prefill_path(m, wq):
     """True when linear() sends m rows to the int4 prefill GEMM rather than dequantize + BLAS (auto routing only)."""
     if auto_version(m, wq) is not None or wq.packed_mma is None:
         return False
-    return wq.k >= AUTO_PREFILL_MIN_K or (wq.n >= AUTO_PREFILL_WIDE_N and m <= AUTO_PREFILL_WIDE_ROWS)
+    return (wq.k >= AUTO_PREFILL_MIN_K or m <= AUTO_PREFILL_ROWS
+            or (m <= AUTO_PREFILL_NARROW_ROWS and wq.n <= AUTO_PREFILL_NARROW and wq.k <= AUTO_PREFILL_NARROW))
 
 
 def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     """Decode (few rows): an INT4 kernel (v6 GEMV for one row, v5 MFMA beyond). Prefill (many rows): dequantize, then
-    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM on long K and on wide N up to 256
-    rows (prefill_path). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5:
+    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM where prefill_path says (long K,
+    up to 256 rows, small layers up to 512 rows). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5:
     64), and dequantize + BLAS above.
     bias (fp16 [N], optional; not in the reference's signature): y = fp16(x W^T) + bias in fp16, the rounding of the
     reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra

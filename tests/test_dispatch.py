@@ -27,11 +27,12 @@ def _rule_cases():
     g, v5, v5w, wide = ops.AUTO_GEMV_ROWS, ops.AUTO_V5_ROWS, ops.AUTO_V5_WIDE_ROWS, ops.AUTO_WIDE_N
     gn, gwide, kmax = ops.AUTO_GEMV_NARROW_ROWS, ops.AUTO_GEMV_NARROW_N, ops.AUTO_GEMV_MAX_K
     narrow, wide_n = max(256, wide // 2), wide
+    past = "prefill" if v5w + 1 <= ops.AUTO_PREFILL_ROWS else "dequant"   # beyond the MFMA kernel's rows
     return [(1, narrow, 256, 6), (g, narrow, 256, 6), (gn, narrow, 256, 6), (gn + 1, narrow, 256, 5),
             (g + 1, gwide, 256, 5), (gn, gwide - 16, 256, 6), (g + 1, narrow, kmax + 128, 5), (gn, narrow, kmax, 6),
-            (1, gwide, kmax + 128, 6), (v5, narrow, 256, 5), (v5 + 1, narrow, 256, "dequant"),
-            (v5 + 1, wide_n, 256, 5 if v5w > v5 else "dequant"), (v5w, wide_n, 256, 5),
-            (v5w + 1, wide_n, 256, "dequant")]
+            (1, gwide, kmax + 128, 6), (v5, narrow, 256, 5), (v5 + 1, narrow, 256, past),
+            (v5 + 1, wide_n, 256, 5 if v5w > v5 else past), (v5w, wide_n, 256, 5),
+            (v5w + 1, wide_n, 256, past)]
 
 
 @pytest.mark.parametrize("m,n,k,want", _rule_cases())
@@ -41,9 +42,11 @@ def test_auto_rule_on_the_mma_layout(calls, m, n, k, want):
 
 
 def test_reference_table_with_the_t4_constants(calls, monkeypatch):
-    """The rule's structure reproduces the reference's own table when given the reference's (T4) constants."""
+    """The rule's structure reproduces the reference's own table when given the reference's (T4) constants (and no
+    int4 prefill GEMM, which the reference does not have)."""
     for name, value in (("AUTO_GEMV_ROWS", 1), ("AUTO_V5_ROWS", 32), ("AUTO_V5_WIDE_ROWS", 64), ("AUTO_WIDE_N", 3072),
-                        ("AUTO_GEMV_NARROW_ROWS", 1)):
+                        ("AUTO_GEMV_NARROW_ROWS", 1), ("AUTO_PREFILL_ROWS", 0), ("AUTO_PREFILL_NARROW_ROWS", 0),
+                        ("AUTO_PREFILL_MIN_K", 1 << 30)):
         monkeypatch.setattr(ops, name, value)
     for m, n, want in [(1, 1024, 6), (2, 1024, 5), (32, 1024, 5), (33, 1024, "dequant"), (33, 4096, 5), (64, 4096, 5),
                        (65, 4096, "dequant")]:
@@ -53,29 +56,24 @@ def test_reference_table_with_the_t4_constants(calls, monkeypatch):
 
 
 def test_prefill_rule(calls):
-    """Beyond the MFMA kernel's rows, long-K weights on the mma layout take the int4 prefill GEMM; short K, other
-    layouts and fixed versions keep dequantize + BLAS; decode rows never reach it."""
-    kmin, rows = ops.AUTO_PREFILL_MIN_K, ops.AUTO_V5_ROWS + 1
-    for m, k, layouts, version, want in [(rows, kmin, ("mma",), 0, "prefill"), (512, 2 * kmin, ("mma",), 0, "prefill"),
-                                         (rows, kmin - 128, ("mma",), 0, "dequant"), (rows, kmin, ("canonical",), 0, "dequant"),
-                                         (rows, kmin, ("mma",), 5, "dequant"), (1, kmin, ("mma",), 0, 6),
-                                         (rows - 1, kmin, ("mma",), 0, 5)]:
+    """Beyond the MFMA kernel's rows, the int4 prefill GEMM takes long-K weights at any M, every weight up to
+    AUTO_PREFILL_ROWS rows and small layers up to AUTO_PREFILL_NARROW_ROWS; the rest, other layouts and fixed
+    versions keep dequantize + BLAS; decode rows never reach it."""
+    kmin, few, small, small_rows = ops.AUTO_PREFILL_MIN_K, ops.AUTO_PREFILL_ROWS, ops.AUTO_PREFILL_NARROW, \
+        ops.AUTO_PREFILL_NARROW_ROWS
+    rows = ops.AUTO_V5_ROWS + 1
+    big = max(2 * small, 8192)
+    assert small < kmin and few < small_rows
+    for m, n, k, layouts, version, want in [
+            (rows, 1024, kmin, ("mma",), 0, "prefill"), (4096, 1024, 2 * kmin, ("mma",), 0, "prefill"),
+            (few, big, kmin - 128, ("mma",), 0, "prefill"), (few + 1, big, kmin - 128, ("mma",), 0, "dequant"),
+            (small_rows, small, small, ("mma",), 0, "prefill"), (small_rows + 1, small, small, ("mma",), 0, "dequant"),
+            (small_rows, small + 16, small, ("mma",), 0, "dequant"), (small_rows, small, small + 128, ("mma",), 0, "dequant"),
+            (rows, 1024, kmin, ("canonical",), 0, "dequant"), (rows, 1024, kmin, ("mma",), 5, "dequant"),
+            (1, 1024, kmin, ("mma",), 0, 6), (rows - 1, 1024, kmin, ("mma",), 0, 5)]:
         calls.clear()
-        ops.linear(torch.zeros(m, k), weight(1024, k, layouts), version=version)
-        assert calls == [want], (m, k, layouts, version)
-
-
-def test_prefill_rule_for_wide_layers(calls):
-    """Short-K weights with N >= AUTO_PREFILL_WIDE_N take the int4 prefill GEMM up to AUTO_PREFILL_WIDE_ROWS rows,
-    dequantize + BLAS beyond; narrower N never does."""
-    wide, rows, v5 = ops.AUTO_PREFILL_WIDE_N, ops.AUTO_PREFILL_WIDE_ROWS, ops.AUTO_V5_WIDE_ROWS
-    k = 2048
-    assert k < ops.AUTO_PREFILL_MIN_K
-    for m, n, want in [(v5 + 1, wide, "prefill"), (rows, wide, "prefill"), (rows + 1, wide, "dequant"),
-                       (rows, wide - 16, "dequant"), (v5, wide, 5), (rows, 2 * wide, "prefill")]:
-        calls.clear()
-        ops.linear(torch.zeros(m, k), weight(n, k))
-        assert calls == [want], (m, n)
+        ops.linear(torch.zeros(m, k), weight(n, k, layouts), version=version)
+        assert calls == [want], (m, n, k, layouts, version)
 
 
 @pytest.mark.parametrize("layouts,m,want", [(("canonical", "v3"), 1, 4), (("canonical", "v3"), 8, 4),
