@@ -321,14 +321,18 @@ PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes) {
   if (!prefill_fits(p.MT, p.D, p.NW, p.XL)) p.NW = 4;      // 8 waves: 256 registers per wave, D = 2 and MT = 4 only
   if (!prefill_fits(p.MT, p.D, p.NW, p.XL)) p.D = 2;
   p.MG = (M + 16 * p.MT - 1) / (16 * p.MT);
-  // fewer 16-row tiles per wave (default shape only) while the grid holds less than two workgroups per CU. A wave's
-  // activation bytes per chunk stay the same while its weight bytes shrink (x : w = 4 : PT), so past 4 activation
-  // tiles a long K (>= 128 chunks) splits across workgroups instead (measured: 7B down, M = 512, 130 us at 4 tiles
-  // and 2 splits vs 142 at 1 tile; M = 2048, 351 vs 451; at M <= 256 and on K <= 11008 the thin tiles win up to 2.9x)
+  // fewer 16-row tiles per wave (default shape only): 2 up to 8 activation tiles (168 instead of 256 registers, a third
+  // wave per SIMD: 3B merged gate|up at M = 512 89 -> 77 us, 7B gate|up 133 -> 106; at M = 2048 4 tiles stay ahead,
+  // 365 vs 388), then halved while the grid holds less than two workgroups per CU. A wave's activation bytes per
+  // chunk stay the same while its weight bytes shrink (x : w = 4 : PT), so past 4 activation tiles a long K (>= 128
+  // chunks) splits across workgroups instead (7B down, M = 512: 130 us at 4 tiles and 2 splits vs 142 at 1 tile;
+  // M = 2048: 351 vs 451; at M <= 256 and on K <= 11008 the thin tiles win up to 2.9x)
   auto groups = [&](int pt) { return (long)((N + 16 * pt * p.NW - 1) / (16 * pt * p.NW)) * p.MG; };
   p.PT = 4;
-  if (o.waves == 0 && o.ring == 0 && (KC < 128 || p.MG <= 4))
+  if (o.waves == 0 && o.ring == 0 && (KC < 128 || p.MG <= 4)) {
+    if (p.MG <= 8) p.PT = 2;
     while (p.PT > 1 && groups(p.PT) < 2 * kPrefillTargetGroups) p.PT /= 2;
+  }
   const long tiles = groups(p.PT);
   const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
   int S = 1;
