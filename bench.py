@@ -484,7 +484,7 @@ def sweep_gemv(a):
 
 
 def sweep_tiles(a):
-    """MFMA GEMM (v5) per decode shape and M in 2..48: graph-timed us per call of the row-group kernel (automatic
+    """MFMA GEMM (v5) per decode shape and M in 2..64: graph-timed us per call of the row-group kernel (automatic
     shape), of one tile per workgroup with 2, 4 and 8 waves, and of the automatic choice (lowbit_set_gemm_kernel)."""
     import torch
     from lowbit import _native, ops
@@ -493,7 +493,7 @@ def sweep_tiles(a):
     rows = []
     for k, n in SWEEP_SHAPES:
         cl = cloned_copies(torch, ops, k, n)
-        for m in (2, 4, 8, 16, 24, 32, 40, 48):
+        for m in (2, 4, 8, 16, 24, 32, 40, 48, 56, 64):
             x = torch.randn(m, k, device="cuda").half()
             t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5), max(300, len(cl))), 2)
             r = {"K": k, "N": n, "M": m}

@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   }
 }
 
-// gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 48 on attention-sized layers
+// gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 64 on attention-sized layers
 // (few tiles, short K; the selection rule is tiles_win below). The row-group kernel above stages activations for 64
 // rows with a barrier per chunk and, on narrow layers, splits K over workgroups that each pay an agent-scope release to
 // add the partials; here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
@@ -476,7 +476,7 @@ hipError_t dispatch_ring(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 }
 
 // one tile per workgroup, up to 8 waves (the register budget of 2 waves per SIMD): M <= 16 with a 4-deep ring, M <= 32
-// with 3 slots, M <= 48 with 2 (198 registers)
+// with 3 slots, M <= 64 with 2 (198 registers at M <= 48, 255 at M <= 64)
 template <int MT>
 hipError_t launch_tiles(const GemvArgs& a, int waves) {
   constexpr int D = MT == 1 ? 4 : MT == 2 ? 3 : 2, kThreads = 512;
@@ -496,13 +496,13 @@ hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 
 }  // namespace
 
-// One tile per workgroup beats row groups, from an MI355X sweep (graph-timed, cold weights, M = 2..48 on the
+// One tile per workgroup beats row groups, from an MI355X sweep (graph-timed, cold weights, M = 2..64 on the
 // Qwen2.5-1.5B/3B/7B projections; bench.py --sweep tiles), on the attention-sized layers: up to 288 tiles (N <= 4608)
 // and K short enough that every wave's own activation loads (4 KB per 1 KB of weights per 16 rows of M) stay cheap,
-// KC * MT <= 56 (K <= 3584 up to M = 32, K <= 2304 up to M = 48): 1.1-2.4x (2048 x 2560, M = 16: 13.3 -> 5.6 us;
-// M = 48, where row groups split K over workgroups: 18.5 -> 10.7 us). Long K (8960 and up) or wide N keep row groups,
-// which share the activations through LDS.
-bool tiles_win(int MT, int ntiles, int KC) { return MT <= 3 && ntiles <= 288 && KC * MT <= 56; }
+// KC * MT <= 64 (K <= 3584 up to M = 32, K <= 2048 up to M = 64): 1.1-2.4x (2048 x 2560, M = 16: 13.3 -> 5.6 us;
+// M = 48 and 64, where row groups split K over workgroups: 18.5 -> 10.7 and 20.1 -> 13.1 us). Long K (8960 and up,
+// or 3584 from 33 rows) and wide N keep row groups, which share the activations through LDS.
+bool tiles_win(int MT, int ntiles, int KC) { return MT <= 4 && ntiles <= 288 && KC * MT <= 64; }
 
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
 // tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
@@ -515,7 +515,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   const GemvOverride o = gemv_override();
   const int ntiles = (N + 15) / 16, KC = K / 128;
   p.MT = (M + 15) / 16;
-  if (p.MT <= 3 && row_tiles == 0 && (o.gemm_kernel == 2 || (o.gemm_kernel == 0 && tiles_win(p.MT, ntiles, KC)))) {
+  if (p.MT <= 4 && row_tiles == 0 && (o.gemm_kernel == 2 || (o.gemm_kernel == 0 && tiles_win(p.MT, ntiles, KC)))) {
     int waves = ntiles <= 256 && KC >= 24 ? 8 : 4;            // same sweep
     if (o.waves > 0) waves = o.waves;
     waves = std::min(waves, 8);
@@ -555,7 +555,9 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
 
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
   const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
-  if (p.TW > 0) return p.MT == 1 ? launch_tiles<1>(a, p.TW) : p.MT == 2 ? launch_tiles<2>(a, p.TW) : launch_tiles<3>(a, p.TW);
+  if (p.TW > 0)
+    return p.MT == 1 ? launch_tiles<1>(a, p.TW) : p.MT == 2 ? launch_tiles<2>(a, p.TW)
+         : p.MT == 3 ? launch_tiles<3>(a, p.TW) : launch_tiles<4>(a, p.TW);
   uint32_t* ctr = static_cast<uint32_t*>(workspace);
   float* part = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes) : nullptr;
   switch (p.MT) {
