@@ -498,8 +498,8 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_
   // per wave always. A layer with at most 128 tiles and K >= 2048 splits each tile over the most workgroups (2 or 4)
   // that still fit one round of the 256 CUs: the decode ALU work of its busiest CU then halves or quarters (8960 x
   // 1536: 5.5 -> 4.3 us, 11008 x 2048: 6.1 -> 4.9 us); a split that leaves a CU two workgroups, or a short K, gains
-  // nothing. 8 waves splitting K on narrow and split layers (16 on long rows), fewer as the tile count grows so that
-  // about 3k waves are in flight; never more waves than wave-loads; 4 wave-loads in flight per wave.
+  // nothing. 8 waves splitting K on narrow and split layers (16 on long rows), fewer as the tile count grows (below);
+  // never more waves than wave-loads; 4 wave-loads in flight per wave.
   p.R = rows_per_wave ? rows_per_wave : 1;
   auto split_fits = [&](int cs) { return p.R == 1 && row_split_ok && KC % cs == 0; };
   if (o.splits == 1 || ((o.splits == 2 || o.splits == 4) && split_fits(o.splits))) {
@@ -511,8 +511,11 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_
   const int blocks = p.CS == 1 ? (ntiles + p.R - 1) / p.R : ntiles * p.CS;
   int waves;
   if (p.CS == 1 && blocks >= 256) {
+    // about 1.5k waves in flight, at most 16 wave-loads each (2048 x 22016: 1 wave, 6.4 vs 7.0 us at 2; 2048 x 11008:
+    // 2, 4.6 vs 4.8 at 4; 3584 x 4608: 4, 4.2 vs 4.5 at 8; 3584 x 18944 keeps 2: 28 wave-loads on 1 wave take 10.3 us)
     waves = 1;
-    while (waves < 8 && blocks * waves * 2 <= 3072) waves *= 2;
+    while (waves < 8 && blocks * waves * 2 <= 1536) waves *= 2;
+    while (waves < 8 && KC / waves > 16) waves *= 2;
   } else {
     waves = KC / p.CS >= 128 ? 16 : 8;
   }
