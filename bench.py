@@ -41,7 +41,7 @@ HBM_PEAK_GBPS = 8000.0
 # HBM bytes per GEMV launch of this workload, measured: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
 # `bench.py --pmc-workload` (20 eager steps), each scaled by what the counter reads for a 1 GiB elementwise copy in the
 # same run (FETCH x2.0, WRITE x1.0); 1.032x the algorithmic bytes. Re-measure when the kernel changes.
-TRAFFIC_PER_LAUNCH = 4721267
+TRAFFIC_PER_LAUNCH = 4723463
 MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
 
 
