@@ -62,11 +62,12 @@ int check_common(const void* x, const void* w, const void* s, const void* y, int
 }
 
 // 32-bit buffer offsets bound K and the scale count for the MFMA-layout kernels; the GEMV also stages the scales of
-// its rows in LDS, which bounds K / G
-int check_mfma_layout_limits(int64_t N, int64_t K, int64_t group, bool gemv) {
+// its tiles in LDS (16 rows x K / G fp16 per tile, gemv_tiles tiles per wave; 0 = not the GEMV), which bounds K / G
+int check_mfma_layout_limits(int64_t N, int64_t K, int64_t group, int gemv_tiles) {
   if (K > kMaxK) return fail(LOWBIT_ERR_SHAPE, "K is at most %lld for the MFMA-layout kernels", (long long)kMaxK);
-  if (gemv && K / group > kMaxGroups)
-    return fail(LOWBIT_ERR_GROUP, "K / group is at most %d for the v6 GEMV", kMaxGroups);
+  if (gemv_tiles > 0 && (int64_t)16 * gemv_tiles * (K / group) * 2 > (int64_t)kGemvLdsX)
+    return fail(LOWBIT_ERR_GROUP, "K / group is at most %d for the v6 GEMV with %d tile(s) per wave",
+                kMaxGroups / gemv_tiles, gemv_tiles);
   if (N * (K / group) * 2 > INT_MAX) return fail(LOWBIT_ERR_SHAPE, "N * K / group scales exceed 2^30");
   return LOWBIT_OK;
 }
@@ -79,10 +80,10 @@ int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
   if (!((version >= 1 && version <= 4) || version == 6)) return fail(LOWBIT_ERR_VERSION, "version is 1..4 or 6");
   if (version == 6 && (K % 128 || group % 128))
     return fail(LOWBIT_ERR_LAYOUT, "v6 needs K and the group size to be multiples of 128");
-  if (version == 6)
-    if (int rc = check_mfma_layout_limits(N, K, group, true)) return rc;
   if (!(rows_per_wave == 0 || rows_per_wave == 1 || rows_per_wave == 2 || rows_per_wave == 4))
     return fail(LOWBIT_ERR_TUNING, "rows_per_warp is 0 (auto), 1, 2 or 4");
+  if (version == 6)
+    if (int rc = check_mfma_layout_limits(N, K, group, rows_per_wave ? rows_per_wave : 1)) return rc;
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
              (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
@@ -91,14 +92,20 @@ int gemv_impl(const void* x, const void* w, const void* s, void* y, int64_t M, i
   return hip_status(e, "w4_gemv");
 }
 
-int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
-              int row_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+int check_gemm(const void* x, const void* w, const void* s, const void* y, int64_t M, int64_t N, int64_t K,
+               int64_t group, int row_tiles) {
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the MFMA kernel takes 1..64 rows");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "v5 needs K and the group size to be multiples of 128");
-  if (int rc = check_mfma_layout_limits(N, K, group, false)) return rc;
+  if (int rc = check_mfma_layout_limits(N, K, group, 0)) return rc;
   if (!(row_tiles == 0 || row_tiles == 1 || row_tiles == 2 || row_tiles == 4))
     return fail(LOWBIT_ERR_TUNING, "row_tiles must be 1, 2 or 4");
+  return LOWBIT_OK;
+}
+
+int gemm_impl(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K, int64_t group,
+              int row_tiles, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_gemm(x, w, s, y, M, N, K, group, row_tiles)) return rc;
   if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
     return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
   if (int rc = check_device()) return rc;
@@ -233,7 +240,7 @@ int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y,
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the fused projection takes 1..64 rows");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
-  if (int rc = check_mfma_layout_limits(N, K, group, M == 1)) return rc;
+  if (int rc = check_mfma_layout_limits(N, K, group, M == 1 ? 1 : 0)) return rc;
   if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
   if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
     return fail(LOWBIT_ERR_ARG, "the bias and residual epilogues need aux");
@@ -260,7 +267,7 @@ int lowbit_w4_gemm_prefill(const void* x, const void* w, const void* s, void* y,
   if (int rc = check_common(x, w, s, y, M, N, K, group)) return rc;
   if (M < 1) return fail(LOWBIT_ERR_ROWS, "the prefill GEMM takes at least one row");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
-  if (int rc = check_mfma_layout_limits(N, K, group, false)) return rc;
+  if (int rc = check_mfma_layout_limits(N, K, group, 0)) return rc;
   if ((M + 128) * K * 2 > INT_MAX) return fail(LOWBIT_ERR_SHAPE, "the prefill GEMM takes (M + 128) * K * 2 < 2^31");
   if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
   if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
@@ -308,7 +315,7 @@ int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, i
   if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || N != (Hq + 2 * Hkv) * 128 || !fits_int(L * 128 * Hkv))
     return fail(LOWBIT_ERR_SHAPE, "qkv_rope: N must be (Hq + 2 Hkv) * 128 with Hkv dividing Hq, L positive");
   if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
-  if (int rc = check_mfma_layout_limits(N, K, group, true)) return rc;
+  if (int rc = check_mfma_layout_limits(N, K, group, 1)) return rc;
   if (norm_weight && (K > 16384 || !aligned16(norm_weight)))
     return fail(LOWBIT_ERR_ARG, "the fused input norm takes K <= 16384 and a 16-byte aligned weight");
   if (int rc = check_device()) return rc;

@@ -116,6 +116,21 @@ WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (16 << 20)     # LOWBIT_WORKSPACE_BY
 PREFILL_WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (64 << 20)
 ATTENTION_WORKSPACE_BYTES = 4 << 20
 _WORKSPACES = {}
+_CAPTURE_STREAMS = {}
+
+
+def capture_stream(device):
+    """One side stream per device on which the decoders warm up and capture their graphs. Workspaces are keyed by
+    stream, so warming up on the stream that is then captured creates every workspace before capture (no allocation
+    or fill kernel lands in a graph), and later captures reuse them. Graphs captured on it share those workspaces,
+    so they must not be replayed concurrently (replay them on one stream)."""
+    import torch
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    s = _CAPTURE_STREAMS.get(index)
+    if s is None:
+        s = torch.cuda.Stream(device=torch.device("cuda", index))
+        _CAPTURE_STREAMS[index] = s
+    return s
 
 
 def workspace(device, stream, nbytes=WORKSPACE_BYTES):
@@ -129,6 +144,40 @@ def workspace(device, stream, nbytes=WORKSPACE_BYTES):
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _WORKSPACES[key] = ws
     return ws
+
+
+def _check_epilogue(epilogue, aux, m, n, device):
+    """aux must match what the kernels read: bias [N] or residual [M, N], fp16, contiguous, on x's GPU (the C ABI
+    cannot check its size)."""
+    import torch
+    if epilogue not in (EPI_STORE, EPI_BIAS, EPI_RESIDUAL, EPI_SILU_MUL):
+        raise RuntimeError("unknown epilogue")
+    if epilogue in (EPI_BIAS, EPI_RESIDUAL):
+        if aux is None:
+            raise RuntimeError("the bias and residual epilogues need aux")
+        if aux.dtype != torch.float16 or not aux.is_contiguous() or aux.device != device:
+            raise RuntimeError("aux must be a contiguous float16 tensor on the same GPU")
+        if epilogue == EPI_BIAS and aux.numel() != n:
+            raise RuntimeError(f"bias must hold N={n} values, got {aux.numel()}")
+        if epilogue == EPI_RESIDUAL and (aux.dim() != 2 or tuple(aux.shape) != (m, n)):
+            raise RuntimeError(f"the residual must be [M, N] = [{m}, {n}], got {list(aux.shape)}")
+
+
+def _need(t, name, dtype, shape, device):
+    """t must be a contiguous tensor of `dtype` and `shape` on `device` (the kernels index it by that shape)."""
+    if t is None or t.dtype != dtype or not t.is_contiguous() or t.device != device or tuple(t.shape) != tuple(shape):
+        got = "None" if t is None else f"{t.dtype} {list(t.shape)} on {t.device}"
+        raise RuntimeError(f"{name} must be a contiguous {dtype} tensor of shape {list(shape)} on {device}, got {got}")
+
+
+def _check_norm(norm, k, device):
+    """The fused input norm's weight: fp16 [K], contiguous, on x's GPU."""
+    import torch
+    if norm is None:
+        return
+    nw = norm[0]
+    if nw.dtype != torch.float16 or not nw.is_contiguous() or nw.device != device or nw.numel() != k:
+        raise RuntimeError(f"the norm weight must be a contiguous float16 [K={k}] tensor on the same GPU")
 
 
 def _check_tensors(x, w, s, group):
@@ -244,10 +293,10 @@ class NativeExt:
         m, n = x.shape[0], w.shape[0]
         cols = n // 2 if epilogue == EPI_SILU_MUL else n
         y = out if out is not None else torch.empty((m, cols), dtype=torch.float16, device=x.device)
-        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous():
+        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous() or y.device != x.device:
             raise RuntimeError("out must be a contiguous float16 [M, N] (or [M, N/2] for silu-mul) tensor")
-        if aux is not None and (aux.dtype != torch.float16 or not aux.is_contiguous() or aux.device != x.device):
-            raise RuntimeError("aux must be a contiguous float16 tensor on the same GPU")
+        _check_epilogue(epilogue, aux, m, n, x.device)
+        _check_norm(norm, x.shape[1], x.device)
         with _DeviceGuard(x.device):
             st = _stream(x.device)
             ws = workspace(x.device, st)
@@ -266,10 +315,9 @@ class NativeExt:
         m, n = x.shape[0], w.shape[0]
         cols = n // 2 if epilogue == EPI_SILU_MUL else n
         y = out if out is not None else torch.empty((m, cols), dtype=torch.float16, device=x.device)
-        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous():
+        if y.shape != (m, cols) or y.dtype != torch.float16 or not y.is_contiguous() or y.device != x.device:
             raise RuntimeError("out must be a contiguous float16 [M, N] (or [M, N/2] for silu-mul) tensor")
-        if aux is not None and (aux.dtype != torch.float16 or not aux.is_contiguous() or aux.device != x.device):
-            raise RuntimeError("aux must be a contiguous float16 tensor on the same GPU")
+        _check_epilogue(epilogue, aux, m, n, x.device)
         with _DeviceGuard(x.device):
             st = _stream(x.device)
             ws = workspace(x.device, st, PREFILL_WORKSPACE_BYTES)
@@ -280,13 +328,33 @@ class NativeExt:
 
     def rmsnorm(self, x, weight, eps, out=None):
         import torch
+        if not x.is_cuda or x.dim() != 2:
+            raise RuntimeError("rmsnorm takes a 2-D CUDA tensor x [M, H]")
+        _need(x, "x", torch.float16, x.shape, x.device)
+        _need(weight, "the norm weight", torch.float16, (x.shape[1],), x.device)
         y = out if out is not None else torch.empty_like(x)
+        _need(y, "out", torch.float16, x.shape, x.device)
         with _DeviceGuard(x.device):
             check(self.lib.lowbit_rmsnorm(ptr(x), ptr(weight), ptr(y), x.shape[0], x.shape[1], float(eps),
                                           _stream(x.device)))
         return y
 
+    def _check_rope(self, m, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, device):
+        import torch
+        if k_cache.dim() != 3:
+            raise RuntimeError("the caches must be [Hkv, L, 128]")
+        _need(positions, "positions", torch.int64, (m,), device)
+        _need(inv_freq, "inv_freq", torch.float32, (64,), device)
+        _need(q_out, "q_out", torch.float16, (m, hq, 128), device)
+        _need(k_cache, "k_cache", torch.float16, (hkv, k_cache.shape[1], 128), device)
+        _need(v_cache, "v_cache", torch.float16, tuple(k_cache.shape), device)
+
     def rope_kv(self, qkv, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, permuted=False):
+        import torch
+        if not qkv.is_cuda or qkv.dim() != 2:
+            raise RuntimeError("qkv must be a 2-D CUDA tensor [M, (Hq + 2 Hkv) 128]")
+        _need(qkv, "qkv", torch.float16, (qkv.shape[0], (hq + 2 * hkv) * 128), qkv.device)
+        self._check_rope(qkv.shape[0], positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, qkv.device)
         with _DeviceGuard(qkv.device):
             check(self.lib.lowbit_rope_kv(ptr(qkv), ptr(positions), ptr(inv_freq), ptr(q_out), ptr(k_cache),
                                           ptr(v_cache), qkv.shape[0], hq, hkv, k_cache.shape[1], int(bool(permuted)),
@@ -295,9 +363,15 @@ class NativeExt:
     def w4_qkv_rope(self, x, w, s, group, bias, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, norm=None):
         """One token: the RoPE-permuted q|k|v projection (+ bias, RoPE, cache write) into q_out [1, Hq, 128] and
         the caches [Hkv, L, 128]; norm = (weight, eps) normalizes x first."""
+        import torch
         _check_tensors(x, w, s, group)
         if x.shape[0] != 1:
             raise RuntimeError("w4_qkv_rope takes one row")
+        if w.shape[0] != (hq + 2 * hkv) * 128:
+            raise RuntimeError("the q|k|v weight must have (Hq + 2 Hkv) * 128 rows")
+        _need(bias, "bias", torch.float16, (w.shape[0],), x.device)
+        _check_norm(norm, x.shape[1], x.device)
+        self._check_rope(1, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, x.device)
         nw, eps = norm if norm is not None else (None, 0.0)
         with _DeviceGuard(x.device):
             check(self.lib.lowbit_w4_qkv_rope(ptr(x), ptr(w), ptr(s), w.shape[0], x.shape[1], group, ptr(bias),
@@ -307,6 +381,15 @@ class NativeExt:
 
     def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale, split=True):
         """split=False runs one block per (token, head group), without the key partitions and their workspace."""
+        import torch
+        if not q.is_cuda or q.dim() != 3 or k_cache.dim() != 3:
+            raise RuntimeError("q [M, Hq, 128] and the caches [Hkv, L, 128] must be CUDA tensors")
+        m = q.shape[0]
+        _need(q, "q", torch.float16, (m, hq, 128), q.device)
+        _need(k_cache, "k_cache", torch.float16, (hkv, k_cache.shape[1], 128), q.device)
+        _need(v_cache, "v_cache", torch.float16, tuple(k_cache.shape), q.device)
+        _need(positions, "positions", torch.int64, (m,), q.device)
+        _need(out, "out", torch.float16, (m, hq * 128), q.device)
         with _DeviceGuard(q.device):
             st = _stream(q.device)
             ws = workspace(q.device, st, ATTENTION_WORKSPACE_BYTES) if split else None
@@ -325,6 +408,7 @@ class NativeExt:
         if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1]:
             raise RuntimeError("x [M, K] and w [N, K]")
         y = out if out is not None else torch.empty((x.shape[0], w.shape[0]), dtype=torch.float16, device=x.device)
+        _need(y, "out", torch.float16, (x.shape[0], w.shape[0]), x.device)
         with _DeviceGuard(x.device):
             check(self.lib.lowbit_f16_gemv(ptr(x), ptr(w), ptr(y), x.shape[0], w.shape[0], x.shape[1],
                                            _stream(x.device)))

@@ -8,6 +8,8 @@ picked on the GPU inside the graph (argmax), so greedy decoding never synchroniz
 """
 import torch
 
+from . import _native
+
 QWEN25 = {
     # hidden, intermediate, layers, query heads, kv heads (head_dim 128 throughout)
     "1.5b": (1536, 8960, 28, 12, 2),
@@ -95,14 +97,15 @@ class GraphDecoder:
 
     @torch.inference_mode()
     def capture(self, warmup=3):
-        """Warm up on a side stream (first calls allocate the cache layers and the library's workspaces), then
-        capture one step. Must follow a prefill; the warm-up writes into cache rows past the prompt, which every
+        """Warm up on the capture stream (first calls allocate the cache layers and the library's workspaces), then
+        capture one step on the same stream. Must follow a prefill; the warm-up writes into cache rows past the prompt, which every
         real step overwrites before reading. Each replay then advances the cache's write position and the decoder's
         position together."""
         if self.pos + self.chunk > self.max_len:
             raise ValueError("the static cache has no room for a step after the prefill")
         self.positions.copy_(self.offsets + self.pos)
-        s = torch.cuda.Stream()
+        # warm-up and capture on one stream, so the library's workspaces (keyed by stream) exist before capture
+        s = _native.capture_stream(self.tokens.device)
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(warmup):
@@ -111,7 +114,7 @@ class GraphDecoder:
             self._sync_write_position()
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=s):
             self.logits = self._forward()
             self.next_token = self.logits[-1].argmax(-1)
         return self

@@ -61,7 +61,7 @@ class _W4:
         if ops.prefill_path(x.shape[0], wq):                 # the int4 prefill GEMM, epilogue fused
             return ops.ext().w4_gemm_prefill(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out)
         w = ops.dequant(wq)                                  # prefill: dequantize + hipBLASLt, epilogue in torch
-        return _torch_epilogue(x, w, epilogue, aux, out)
+        return _torch_epilogue(x, w, epilogue, aux, out, round_first=True)
 
 
 class _F16:
@@ -74,7 +74,15 @@ class _F16:
         return _torch_epilogue(x, self.w, epilogue, aux, out)
 
 
-def _torch_epilogue(x, w, epilogue, aux, out):
+def _torch_epilogue(x, w, epilogue, aux, out, round_first=False):
+    """The epilogues through torch. round_first: round the product to fp16, then add the bias or residual in fp16
+    (the int4 kernels' rounding, so a W4A16 layer rounds alike on every route); otherwise fold the addend into addmm
+    (one rounding, as nn.Linear with a bias does), which the fp16 projections use."""
+    if round_first and epilogue in (EPI_BIAS, EPI_RESIDUAL):
+        y = F.linear(x, w)
+        if epilogue == EPI_BIAS:
+            return torch.add(y, aux, out=out) if out is not None else y.add_(aux)
+        return out.add_(y) if out is not None and out.data_ptr() == aux.data_ptr() else torch.add(aux, y, out=out)
     if epilogue == EPI_BIAS:
         return torch.addmm(aux, x, w.t(), out=out) if out is not None else torch.addmm(aux, x, w.t())
     if epilogue == EPI_RESIDUAL:
@@ -214,14 +222,15 @@ class FusedDecoder:
         if self.pos + self.chunk > self.f.max_len:
             raise ValueError("the cache has no room for a step after the prefill")
         self.positions.copy_(self.offsets + self.pos)
-        s = torch.cuda.Stream()
+        # warm-up and capture on one stream, so the library's workspaces (keyed by stream) exist before capture
+        s = _native.capture_stream(self.tokens.device)
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(warmup):
                 self.f(self.tokens, self.positions)
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=s):
             self.logits = self.f(self.tokens, self.positions)
             self.next_token = self.logits[-1].argmax(-1)
             if self.chunk == 1:

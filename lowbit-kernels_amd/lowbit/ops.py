@@ -210,12 +210,16 @@ def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM where prefill_path says (long K,
     up to 256 rows, small layers up to 512 rows). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5:
     64), and dequantize + BLAS above.
-    bias (fp16 [N], optional; not in the reference's signature): y = fp16(x W^T) + bias in fp16, the rounding of the
-    reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra
+    bias ([N], optional; not in the reference's signature; used in fp16 on x's device on every route): y =
+    fp16(x W^T) + bias in fp16, the rounding of the reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra
     launch), multi-row v6 and dequantize + BLAS with a separate add."""
     m = x.shape[0]
     if m == 0:
         return x.new_empty(0, wq.n)
+    if bias is not None:                      # one bias for every route: fp16 [N] on x's device
+        if bias.numel() != wq.n:
+            raise ValueError(f"bias must hold N={wq.n} values, got shape {list(bias.shape)}")
+        bias = bias.reshape(wq.n).to(device=x.device, dtype=torch.float16).contiguous()
     if version == 0:
         v = auto_version(m, wq)
     elif version in MAX_ROWS:

@@ -165,11 +165,23 @@ OVERFLOW_CASE = {"k": 128, "n": 16, "byte": 0xFF, "scale": 2.0 ** -10, "answers"
                  "tol": 2.0}
 
 
-def cpu_linear_path(x16, w32, group=128):
-    """The reference's CPU torch path for one layer, as BASELINE configs[0] states it: quantize (lowbit/quant.py:23-35),
-    dequantize to fp16 (lowbit/ops.py:119-123), torch.nn.functional.linear. Returns (y fp16 [M, N], packed, scales)."""
+def dequantize_w4_torch(packed, scales, group=128):
+    """The reference's torch dequantize (lowbit/ops.py:119-123), restated for the CPU baseline: each nibble as a float32
+    u - 8, times its group's scale in float32, rounded once to fp16 -> torch fp16 [N, K]. Runs on torch's CPU kernels
+    (all of torch's threads), as the reference's CPU path does; bit-identical to dequantize_w4_f16."""
     import torch
-    packed, scales = quantize_w4(w32, group)
-    w16 = torch.from_numpy(dequantize_w4_f16(packed, scales, group))
-    y = torch.nn.functional.linear(torch.as_tensor(x16), w16)
-    return y, packed, scales
+    p = torch.as_tensor(np.ascontiguousarray(packed))
+    s = torch.as_tensor(np.ascontiguousarray(scales))
+    n, half_k = p.shape
+    u = torch.empty(n, 2 * half_k, dtype=torch.float32)
+    u[:, 0::2] = p & 0xF
+    u[:, 1::2] = p >> 4
+    u -= OFFSET
+    return (u.view(n, -1, group) * s.float().unsqueeze(-1)).view(n, 2 * half_k).half()
+
+
+def cpu_torch_linear(x16, packed, scales, group=128):
+    """One layer of the reference's CPU torch path after quantization: dequantize_w4_torch, then
+    torch.nn.functional.linear on fp16 (reference lowbit/ops.py:119-123,178)."""
+    import torch
+    return torch.nn.functional.linear(torch.as_tensor(x16), dequantize_w4_torch(packed, scales, group))

@@ -49,6 +49,10 @@ def _msg(rc):
      1, "workspace"),
     (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 0, FAKE, 4096, None), 1, "workspace"),
     (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 1 << 23, 128, 0, None, 0, None), 3, "K is at most"),
+    # the v6 GEMV stages 16 x K / G scales per tile in 64 KiB of LDS: 2 tiles per wave halve the K / G it takes
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 1536 * 128, 128, 6, 2, None), 2, "at most 1024"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 600 * 128, 128, 6, 4, None), 2, "at most 512"),
+    (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 2049 * 128, 128, 6, 0, None), 2, "at most 2048"),
     (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 128, -1, 0, None), 2, "positive group size"),
     (lambda l: l.lowbit_w4_dequant(FAKE, FAKE, FAKE, 16, 96, 32, 1, None), 7, "group % 128"),
     (lambda l: l.lowbit_w4_quantize(FAKE, 0, FAKE, FAKE, 16, 128, 2048, None, 0, None), 2, "multiple of the group"),

@@ -1,0 +1,184 @@
+"""The full-size decoders of BASELINE configs[3] and configs[4] on the GPU: random-init Qwen2.5-1.5B architecture
+(28 layers, hidden 1536, 12 / 2 heads, vocab 151936; 64-token prompt) and Qwen2.5-3B architecture (36 layers,
+hidden 2048, 16 / 2 heads; 512-token prompt), every projection int4 g128 with the clip search, the way the reference
+checks its decode path (bench/e2e.py:219-250):
+
+* teacher-forced: the same 96 tokens fed after the prompt at 1, 16 (and for 3B 48) tokens per step through the
+  W4Linear drop-in (GraphDecoder, hipGraph replays) and through FusedQwen2 (FusedDecoder), against the fake-quant
+  model (the same quantized weights dequantized to fp16, PyTorch arithmetic) fed all 96 at once. The yardstick is
+  that model's own noise floor: the same fake-quant model fed one token per step, which changes nothing but fp16
+  summation order and rounding, through 28 or 36 layers. The worst logit difference (max over 96 x 151936 logits,
+  relative to their RMS) must stay within max(2e-2, 2 x the floor's), next-token (argmax) agreement at least 95%;
+* every graph replay gives the bits of the same step run eagerly;
+* greedy decoding of 32 tokens with the argmax taken inside the graph equals eager greedy decoding step by step.
+
+Random-init logits are nearly flat, so near-ties decide some argmaxes; the reference's figure for real checkpoints
+is 99.6-99.8% agreement with the worst logit difference at 2.3% of RMS (results/RESULTS.md:163-165)."""
+import pytest
+import torch
+
+from lowbit import decode, fused, model as lbmodel
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+CLIP = tuple(round(1.0 - 0.025 * i, 3) for i in range(11))     # 1.00 .. 0.75 (reference bench/e2e.py:30)
+FEED, GREEDY = 96, 32
+CONFIGS = {"1.5b": (64, (1, 16)), "3b": (512, (1, 16, 48))}    # prompt tokens, tokens per step
+LOGIT_BOUND, AGREEMENT, FLOOR_FACTOR = 2e-2, 0.95, 2.0
+
+
+def rel_max(a, b):
+    return float((a.float() - b.float()).abs().max() / b.float().pow(2).mean().sqrt())
+
+
+def agreement(a, b):
+    return float((a.argmax(-1) == b.argmax(-1)).float().mean())
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+class Built:
+    """One config: the W4Linear model, FusedQwen2 int4 on the same quantized weights, the prompt, the fed tokens and
+    the fake-quant teacher-forced logits."""
+
+    def __init__(self, name, seed):
+        prompt_len, self.chunks = CONFIGS[name]
+        torch.cuda.set_device(0)
+        say(f"[{name}] building the random-init model")
+        m = decode.random_model(name, seed=seed)
+        vocab = m.config.vocab_size
+        gen = torch.Generator(device="cuda").manual_seed(seed + 100)
+        self.prompt = torch.randint(0, vocab, (1, prompt_len), generator=gen, device="cuda")
+        self.feed = torch.randint(0, vocab, (FEED,), generator=gen, device="cuda")
+        self.max_len = prompt_len + FEED + 16
+        say(f"[{name}] FusedQwen2 int4 (clip search)")
+        self.fused = fused.FusedQwen2(m, self.max_len, quant="int4", clip_grid=CLIP)
+        layers = lbmodel.quantize_layers(m, 128, CLIP)
+        lbmodel.apply_fake_quant(layers)
+        say(f"[{name}] fake-quant reference")
+        self.ref = teacher_forced_graphdecoder(m, self, FEED, graph=False)
+        floor = teacher_forced_graphdecoder(m, self, 1, graph=False)
+        self.floor_err, self.floor_agree = rel_max(floor, self.ref), agreement(floor, self.ref)
+        say(f"[{name}] fake-quant 1 vs {FEED} tokens per step: worst logit diff {self.floor_err:.4f} of RMS, "
+            f"argmax agreement {self.floor_agree:.3f}")
+        replaced, _ = lbmodel.apply_int4(layers)
+        assert replaced == 7 * m.config.num_hidden_layers
+        self.model = m
+        # the fused model's per-row quantization of the merged projections gives the W4Linear bits
+        lay0, fl0 = m.model.layers[0], self.fused.layers[0]
+        assert torch.equal(lay0.self_attn.o_proj.wq.packed_mma, fl0["o"].wq.packed_mma)
+        assert torch.equal(lay0.mlp.down_proj.wq.scales, fl0["down"].wq.scales)
+        say(f"[{name}] built")
+
+
+def teacher_forced_graphdecoder(model, b, chunk, graph=True):
+    dec = decode.GraphDecoder(model, b.max_len, chunk)
+    dec.prefill(b.prompt)
+    if graph:
+        dec.capture()
+        return torch.cat([dec.step(b.feed[i:i + chunk]).float().clone() for i in range(0, FEED, chunk)])
+    rows = []
+    for i in range(0, FEED, chunk):
+        dec.tokens.copy_(b.feed[i:i + chunk].view(1, chunk))
+        dec.positions.copy_(dec.offsets + dec.pos)
+        with torch.inference_mode():
+            rows.append(dec._forward().float().clone())
+        dec.pos += chunk
+    return torch.cat(rows)
+
+
+def teacher_forced_fused(b, chunk, graph=True):
+    dec = fused.FusedDecoder(b.fused, chunk)
+    dec.prefill(b.prompt)
+    if graph:
+        dec.capture()
+        return torch.cat([dec.step(b.feed[i:i + chunk]).float().clone() for i in range(0, FEED, chunk)])
+    rows = []
+    for i in range(0, FEED, chunk):
+        pos = torch.arange(dec.pos, dec.pos + chunk, device="cuda")
+        rows.append(b.fused(b.feed[i:i + chunk], pos).float().clone())
+        dec.pos += chunk
+    return torch.cat(rows)
+
+
+@pytest.fixture(scope="module")
+def qwen15b():
+    return Built("1.5b", seed=150)
+
+
+@pytest.fixture(scope="module")
+def qwen3b():
+    return Built("3b", seed=300)
+
+
+def against_fake_quant(b, tag, got, chunk):
+    err, agree = rel_max(got, b.ref), agreement(got, b.ref)
+    say(f"[{tag}] {chunk} tokens per step: worst logit diff {err:.4f} of RMS, argmax agreement {agree:.3f}")
+    bad = []
+    if err > max(LOGIT_BOUND, FLOOR_FACTOR * b.floor_err):
+        bad.append(f"{tag} at {chunk} per step: logit diff {err:.4f} > max({LOGIT_BOUND}, {FLOOR_FACTOR} x "
+                   f"{b.floor_err:.4f})")
+    if agree < AGREEMENT:
+        bad.append(f"{tag} at {chunk} per step: argmax agreement {agree:.3f}")
+    return bad
+
+
+def run_teacher_forced(b, tag):
+    bad = []                                   # every figure is printed before any assertion
+    for chunk in b.chunks:
+        g = teacher_forced_graphdecoder(b.model, b, chunk)
+        bad += against_fake_quant(b, f"{tag} W4Linear", g, chunk)
+        assert torch.equal(g, teacher_forced_graphdecoder(b.model, b, chunk, graph=False)), (tag, chunk)
+        f = teacher_forced_fused(b, chunk)
+        bad += against_fake_quant(b, f"{tag} FusedQwen2", f, chunk)
+        assert torch.equal(f, teacher_forced_fused(b, chunk, graph=False)), (tag, chunk)
+    assert not bad, bad
+
+
+def run_greedy(b, tag):
+    # FusedDecoder: greedy() replays back to back, the graph feeding its own argmax; eager: the fused forward per step
+    dec = fused.FusedDecoder(b.fused, 1)
+    first = dec.prefill(b.prompt).argmax(-1)
+    dec.capture()
+    toks = dec.greedy(first, GREEDY).tolist()
+    ref = fused.FusedDecoder(b.fused, 1)
+    eager = [int(ref.prefill(b.prompt).argmax(-1))]
+    for _ in range(GREEDY - 1):
+        pos = torch.tensor([ref.pos], device="cuda")
+        eager.append(int(b.fused(torch.tensor([eager[-1]], device="cuda"), pos)[-1].argmax(-1)))
+        ref.pos += 1
+    say(f"[{tag}] FusedQwen2 greedy: {toks[:8]} ...")
+    assert toks == eager
+    # W4Linear under GraphDecoder
+    gd = decode.GraphDecoder(b.model, b.max_len, 1)
+    first = gd.prefill(b.prompt).argmax(-1)
+    gd.capture()
+    toks = gd.greedy(first, GREEDY).tolist()
+    ge = decode.GraphDecoder(b.model, b.max_len, 1)
+    eager = [int(ge.prefill(b.prompt).argmax(-1))]
+    for _ in range(GREEDY - 1):
+        ge.tokens.fill_(eager[-1])
+        ge.positions.copy_(ge.offsets + ge.pos)
+        with torch.inference_mode():
+            eager.append(int(ge._forward()[-1].argmax(-1)))
+        ge.pos += 1
+    say(f"[{tag}] W4Linear greedy: {toks[:8]} ...")
+    assert toks == eager
+
+
+def test_qwen25_1p5b_teacher_forced(cuda, qwen15b):
+    run_teacher_forced(qwen15b, "1.5B")
+
+
+def test_qwen25_1p5b_greedy_graph_equals_eager(cuda, qwen15b):
+    run_greedy(qwen15b, "1.5B")
+
+
+def test_qwen25_3b_teacher_forced(cuda, qwen3b):
+    run_teacher_forced(qwen3b, "3B")
+
+
+def test_qwen25_3b_greedy_graph_equals_eager(cuda, qwen3b):
+    run_greedy(qwen3b, "3B")

@@ -282,3 +282,87 @@ def test_linear_with_bias_equals_linear_then_add(cuda, k, n):
     for m in (1, 3, 16, 64, 96):
         x = torch.randn(m, k, generator=gen).half().cuda()
         assert torch.equal(ops.linear(x, wq, bias=bias), ops.linear(x, wq) + bias), (k, n, m)
+
+
+def test_bias_is_normalised_once_for_every_route(cuda):
+    """linear() casts a bias of another dtype to fp16 on x's device before routing, so every route (fused GEMV, MFMA,
+    dequantize + BLAS) adds the same fp16 values; a bias of the wrong size is refused before any kernel runs."""
+    k, n = 1024, 2560
+    wq, _, *_, gen = make_weight(k, n, 77, layouts=("mma",), sd=0.05)
+    bias32 = torch.randn(n, generator=gen) * 0.5                     # float32, on the CPU
+    for m in (1, 16, 300):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        assert torch.equal(ops.linear(x, wq, bias=bias32), ops.linear(x, wq, bias=bias32.half().cuda())), m
+    with pytest.raises(ValueError, match="bias must hold"):
+        ops.linear(torch.zeros(1, k, dtype=torch.half, device="cuda"), wq, bias=torch.zeros(n - 1))
+
+
+def test_fused_wrappers_refuse_addends_of_the_wrong_size(cuda):
+    """The C ABI cannot see the size of aux or of the norm weight; the binding checks them against N, [M, N] and K."""
+    k, n = 1024, 512
+    wq, *_ = make_weight(k, n, 78, layouts=("mma",))
+    e = ops.ext()
+    x1 = torch.randn(1, k).half().cuda()
+    x4 = torch.randn(4, k).half().cuda()
+    call = lambda x, epi, aux=None, norm=None: e.w4_linear_fused(x, wq.packed_mma, wq.scales, 128, epi, aux,  # noqa
+                                                                  norm=norm)
+    with pytest.raises(RuntimeError, match="bias must hold"):
+        call(x1, fused.EPI_BIAS, torch.zeros(n // 2, dtype=torch.half, device="cuda"))
+    with pytest.raises(RuntimeError, match="residual must be"):
+        call(x4, fused.EPI_RESIDUAL, torch.zeros(1, n, dtype=torch.half, device="cuda"))
+    with pytest.raises(RuntimeError, match="need aux"):
+        call(x4, fused.EPI_BIAS)
+    with pytest.raises(RuntimeError, match="norm weight"):
+        call(x1, fused.EPI_STORE, norm=(torch.ones(k // 2, dtype=torch.half, device="cuda"), 1e-6))
+    with pytest.raises(RuntimeError, match="norm weight"):
+        call(x1, fused.EPI_STORE, norm=(torch.ones(k, dtype=torch.float32, device="cuda"), 1e-6))
+    with pytest.raises(RuntimeError, match="bias must hold"):
+        e.w4_gemm_prefill(torch.randn(96, k).half().cuda(), wq.packed_mma, wq.scales, 128, fused.EPI_BIAS,
+                          torch.zeros(n + 16, dtype=torch.half, device="cuda"))
+    with pytest.raises(RuntimeError, match="norm weight"):
+        e.rmsnorm(x4, torch.ones(k + 8, dtype=torch.half, device="cuda"), 1e-6)
+
+
+def test_w4_torch_fallback_rounds_like_the_kernels(cuda):
+    """Beyond the kernels' rows a fused W4 projection falls back to dequantize + BLAS with the epilogue in torch: the
+    product is rounded to fp16 before the bias or residual is added, as the kernels and linear() + bias do."""
+    k, n, m = 2048, 8192, 600                       # wide, short K, many rows: neither the MFMA nor the prefill GEMM
+    packed, scales = ops.quantize_w4_gpu(torch.randn(n, k, device="cuda") * 0.02, 128)
+    proj = fused._W4(packed, scales, 128)
+    assert m > 64 and not ops.prefill_path(m, proj.wq)
+    x = torch.randn(m, k, device="cuda").half()
+    bias = (torch.randn(n, device="cuda") * 0.5).half()
+    plain = torch.nn.functional.linear(x, ops.dequant(proj.wq))
+    assert torch.equal(proj(x, fused.EPI_BIAS, bias), plain + bias)
+    resid = torch.randn(m, n, device="cuda").half()
+    want = resid + plain
+    assert torch.equal(proj(x, fused.EPI_RESIDUAL, resid.clone()), want)
+    inplace = resid.clone()
+    proj(x, fused.EPI_RESIDUAL, inplace, out=inplace)
+    assert torch.equal(inplace, want)
+
+
+def test_capture_allocates_no_workspace(cuda, tiny_models, monkeypatch):
+    """The decoders warm up on the stream they capture on, so every library workspace exists before capture (no
+    allocation or fill kernel inside a graph), and a second decoder's capture creates none."""
+    created = []
+    real = _native.workspace
+
+    def watching(device, stream, nbytes=_native.WORKSPACE_BYTES):
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes)
+        if key not in _native._WORKSPACES:
+            created.append((key, torch.cuda.is_current_stream_capturing()))
+        return real(device, stream, nbytes)
+
+    monkeypatch.setattr(_native, "workspace", watching)
+    prompt = torch.randint(0, 1024, (1, 20), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda")
+    f = fused.FusedQwen2(tiny_models, 64, quant="int4")
+    for i, chunk in enumerate((1, 16, 1)):
+        dec = fused.FusedDecoder(f, chunk=chunk)
+        dec.prefill(prompt)
+        before = len(_native._WORKSPACES)
+        dec.capture()
+        assert not any(during for _, during in created), created
+        if i == 2:                                  # a second one-token decoder: its capture creates nothing at all
+            assert len(_native._WORKSPACES) == before
+        assert bool(torch.isfinite(dec.step(torch.arange(chunk, device="cuda")).float()).all())

@@ -198,6 +198,31 @@ def test_dequant_f16_is_fp64_product_rounded_once():
             assert got[n, k].view(np.uint16) == want.view(np.uint16)
 
 
+def test_torch_dequant_is_fp64_product_rounded_once():
+    """The reference's torch dequantize, restated for the CPU baseline (dequantize_w4_torch), gives the bits of
+    fp16(fp64 product) element by element: a swapped nibble order, a missing offset or a second rounding fails here."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(109)
+    packed = rng.integers(0, 256, (5, 128), dtype=np.uint8)
+    scales = np.array([[2.0 ** -24, 1.0], [3.1e-5, 6.1e-5], [0.0123, 0.5], [1900.0, 60000.0], [7.0, 0.1]], np.float16)
+    got = R.dequantize_w4_torch(packed, scales, 128)
+    assert got.dtype == torch.float16 and tuple(got.shape) == (5, 256)
+    got = got.numpy()
+    for n in range(5):
+        for k in range(256):
+            u = (int(packed[n, k // 2]) >> (4 * (k % 2))) & 0xF
+            want = np.float16((u - 8) * float(scales[n, k // 128]))
+            assert got[n, k].view(np.uint16) == want.view(np.uint16), (n, k)
+    assert np.array_equal(got.view(np.uint16), R.dequantize_w4_f16(packed, scales, 128).view(np.uint16))
+    w = rng.standard_normal((16, 512)).astype(np.float32)
+    p2, s2 = R.quantize_w4(w, 64)
+    assert np.array_equal(R.dequantize_w4_torch(p2, s2, 64).numpy().view(np.uint16),
+                          R.dequantize_w4_f16(p2, s2, 64).view(np.uint16))
+    x = torch.from_numpy(rng.standard_normal((2, 512)).astype(np.float16))
+    y = R.cpu_torch_linear(x, p2, s2, 64)
+    assert R.rel_err(y.numpy(), R.gemv_reference(x.double().numpy(), p2, s2, 64)) < R.REL_BOUND
+
+
 def test_gemv_reference_brute_force():
     rng = np.random.default_rng(109)
     packed, scales = R.quantize_w4(rng.standard_normal((5, 256)).astype(np.float32), 128)
