@@ -96,6 +96,24 @@ int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t
 int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
                         int64_t group, int row_tiles, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Size of the device scratch lowbit_w4_gemm_mfma_noalloc uses in place of a workspace: the same as
+ * LOWBIT_WORKSPACE_BYTES (16 KiB of arrival counters + 16 MiB of fp32 partial sums). */
+#define LOWBIT_NOALLOC_SCRATCH_BYTES LOWBIT_WORKSPACE_BYTES
+
+/* lowbit_w4_gemm_mfma with no workspace argument and no allocation of any kind: for callers that cannot call
+ * hipMalloc (code under hipGraph capture, tight serving loops, harnesses that forbid allocation). No counterpart in
+ * the reference. The caller passes inputs and outputs; the split-K workspace is a file-scope device array of
+ * LOWBIT_NOALLOC_SCRATCH_BYTES in the library, one per GPU, held until the process ends and found with
+ * hipGetSymbolAddress on the first call on each device. The launch plan is the one lowbit_w4_gemm_mfma makes with a
+ * workspace of that size, so the two give the same bits for the same shape and override. Sizes: 1 <= M <= 64 as
+ * lowbit_w4_gemm_mfma; the partial sums of a K split take S * M * N * 4 bytes and the planner lowers S to what the
+ * scratch holds (M * N <= 131072 keeps the full 32-way split), and a plan that would still not fit is refused with
+ * LOWBIT_ERR_SHAPE. Every call on a GPU shares that GPU's scratch, which keeps the last call's contents: the arrival
+ * counters are cleared by a kernel before first use and every call leaves them zero. Calls that overlap on one GPU
+ * (concurrent streams, or graphs replayed concurrently) race on the scratch and give wrong results: serialize them. */
+int lowbit_w4_gemm_mfma_noalloc(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                                int64_t group, int row_tiles, void* stream);
+
 /* out[N, K] (fp16) = (u - 8) * scale rounded once to fp16, from the canonical (mfma_layout = 0) or the MFMA layout
  * (mfma_layout = 1). Both give the same bits. Replaces the reference's w4_dequant (csrc/w4_gemv.cu:517-540), i.e.
  * ops.dequant (lowbit/ops.py:126-135). */

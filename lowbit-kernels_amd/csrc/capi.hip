@@ -4,6 +4,7 @@
 #include <atomic>
 #include <climits>
 #include <cstring>
+#include <mutex>
 
 #include "kernels.hpp"
 #include "lowbit_w4.h"
@@ -127,6 +128,59 @@ GemvOverride gemv_override() {
 
 }  // namespace lowbit
 
+// ---- the allocation-free MFMA GEMM (lowbit_w4_gemm_mfma_noalloc) ----
+// Its split-K workspace (arrival counters, then fp32 partial sums) is this file-scope device array, the same size as
+// the workspace the Python binding gives lowbit_w4_gemm_mfma, so both entry points plan every shape alike. Each GPU
+// the library runs on holds one copy until the process ends. In host code `scratch` names a host-side stand-in, not
+// the device memory: only the address hipGetSymbolAddress returns for the current device is passed to kernels.
+static __device__ __align__(256) uint8_t scratch[LOWBIT_NOALLOC_SCRATCH_BYTES];
+
+namespace lowbit {
+namespace {
+
+struct ScratchSlot {
+  std::atomic<void*> ptr{nullptr};        // this device's copy of `scratch`
+  std::atomic<bool> cleared{false};       // counters cleared by an executed (not captured) kernel
+};
+ScratchSlot g_scratch[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// The current device's scratch address, looked up once per device with that device current. Its arrival counters
+// must start at zero (every GEMM leaves them zero again): until a clear has run outside graph capture, each call
+// first clears them on its own stream with a kernel (a captured clear is part of its graph and runs before the GEMM
+// on every replay, but does not clear the counters for eager calls).
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(LOWBIT_ERR_DEVICE, "device index %d is beyond %d", dev, kMaxDevices);
+  ScratchSlot& slot = g_scratch[dev];
+  void* p = slot.ptr.load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = slot.ptr.load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !p)
+        return fail(LOWBIT_ERR_HIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      slot.ptr.store(p, std::memory_order_release);
+    }
+  }
+  if (!slot.cleared.load(std::memory_order_acquire)) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &status);
+    if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+    e = zero_words_launch(p, (int)(kCounterBytes / 4), stream);
+    if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "clearing the scratch counters failed: %s", hipGetErrorString(e));
+    if (status == hipStreamCaptureStatusNone) slot.cleared.store(true, std::memory_order_release);
+  }
+  *out = p;
+  return LOWBIT_OK;
+}
+
+}  // namespace
+}  // namespace lowbit
+
 using namespace lowbit;
 
 extern "C" {
@@ -179,6 +233,25 @@ int lowbit_w4_gemv(const void* x, const void* w, const void* s, void* y, int64_t
 int lowbit_w4_gemm_mfma(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
                         int64_t group, int row_tiles, void* workspace, size_t workspace_bytes, void* stream) {
   return gemm_impl(x, w, s, y, M, N, K, group, row_tiles, workspace, workspace_bytes, stream);
+}
+
+int lowbit_w4_gemm_mfma_noalloc(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
+                                int64_t group, int row_tiles, void* stream) {
+  if (int rc = check_gemm(x, w, s, y, M, N, K, group, row_tiles)) return rc;
+  if (int rc = check_device()) return rc;
+  constexpr size_t kScratch = LOWBIT_NOALLOC_SCRATCH_BYTES;
+  // the planner lowers the K split to what the scratch holds; refuse a plan that would not fit it all the same
+  const GemvPlan plan = plan_gemm_mfma((int)M, (int)N, (int)K, row_tiles, kScratch);
+  const int groups = ((int)N + 16 * 4 * plan.R - 1) / (16 * 4 * plan.R);
+  if (plan.S > 1 && ((size_t)plan.S * M * N * sizeof(float) > kScratch - kCounterBytes ||
+                     (size_t)groups * sizeof(uint32_t) > kCounterBytes))
+    return fail(LOWBIT_ERR_SHAPE, "w4_gemm_mfma_noalloc: %d-way split partials of M=%lld x N=%lld exceed the %zu-byte scratch",
+                plan.S, (long long)M, (long long)N, kScratch);
+  void* ws = nullptr;
+  if (int rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &ws)) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
+  return hip_status(gemm_mfma_launch(a, row_tiles, ws, kScratch), "w4_gemm_mfma_noalloc");
 }
 
 int lowbit_w4_dequant(const void* w, const void* s, void* out, int64_t N, int64_t K, int64_t group, int mfma_layout,

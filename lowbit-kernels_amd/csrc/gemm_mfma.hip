@@ -553,6 +553,16 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   return p;
 }
 
+// clears n 32-bit words with vector stores (a kernel rather than a memset, so that it may sit in a captured graph)
+__global__ __launch_bounds__(256) void zero_words(uint32_t* __restrict__ p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0u;
+}
+
+hipError_t zero_words_launch(void* p, int n, hipStream_t stream) {
+  const int blocks = std::max(1, std::min((n + 255) / 256, 64));
+  return launch(zero_words, dim3(blocks), dim3(256), 0, stream, static_cast<uint32_t*>(p), n);
+}
+
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
   const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
   if (p.TW > 0)

@@ -121,6 +121,7 @@ int pick_rows_rowmajor(int N, int M);
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave);
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3);
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes);
+hipError_t zero_words_launch(void* p, int n, hipStream_t stream);
 // prefill variants that compile without register spills (hipcc -O3, gfx950): an 8-wave workgroup has 256 registers
 // per wave, enough for 4 activation tiles and a 2-deep weight ring only
 constexpr bool prefill_fits(int MT, int D, int NW, int XL) {

@@ -28,6 +28,7 @@ SIGNATURES = {
     "lowbit_set_gemm_kernel": ([_int], _int),
     "lowbit_w4_gemv": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp], _int),
     "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp], _int),
+    "lowbit_w4_gemm_mfma_noalloc": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_dequant": ([_vp, _vp, _vp, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_quantize": ([_vp, _int, _vp, _vp, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_float), _int, _vp], _int),
     "lowbit_w4_relayout": ([_vp, _vp, _i64, _i64, _int, _vp], _int),
@@ -228,6 +229,18 @@ class NativeExt:
             ws = workspace(x.device, st)
             check(self.lib.lowbit_w4_gemm_mfma(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group, int(row_tiles),
                                                ptr(ws), ws.numel(), st))
+        return y
+
+    def w4_gemm_tc_noalloc(self, x, w, s, group, row_tiles=0):
+        """w4_gemm_tc through lowbit_w4_gemm_mfma_noalloc: the library's own device scratch instead of a workspace
+        (same bits). Only the output is allocated here; calls on one GPU must not overlap."""
+        import torch
+        _check_tensors(x, w, s, group)
+        m, n = x.shape[0], w.shape[0]
+        y = torch.empty((m, n), dtype=torch.float16, device=x.device)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_w4_gemm_mfma_noalloc(ptr(x), ptr(w), ptr(s), ptr(y), m, n, x.shape[1], group,
+                                                       int(row_tiles), _stream(x.device)))
         return y
 
     def w4_dequant(self, w, s, group, mma_layout=False):

@@ -49,6 +49,10 @@ def _msg(rc):
      1, "workspace"),
     (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 0, FAKE, 4096, None), 1, "workspace"),
     (lambda l: l.lowbit_w4_gemm_mfma(FAKE, FAKE, FAKE, FAKE, 4, 16, 1 << 23, 128, 0, None, 0, None), 3, "K is at most"),
+    (lambda l: l.lowbit_w4_gemm_mfma_noalloc(FAKE, FAKE, FAKE, FAKE, 65, 16, 128, 128, 0, None), 5, "1..64 rows"),
+    (lambda l: l.lowbit_w4_gemm_mfma_noalloc(FAKE, FAKE, FAKE, FAKE, 4, 16, 128, 128, 3, None), 8, "row_tiles"),
+    (lambda l: l.lowbit_w4_gemm_mfma_noalloc(None, FAKE, FAKE, FAKE, 4, 16, 128, 128, 0, None), 1, "null pointer"),
+    (lambda l: l.lowbit_w4_gemm_mfma_noalloc(FAKE, FAKE, FAKE, FAKE, 4, 16, 192, 64, 0, None), 7, "multiples of 128"),
     # the v6 GEMV stages 16 x K / G scales per tile in 64 KiB of LDS: 2 tiles per wave halve the K / G it takes
     (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 1536 * 128, 128, 6, 2, None), 2, "at most 1024"),
     (lambda l: l.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 1, 16, 600 * 128, 128, 6, 4, None), 2, "at most 512"),
