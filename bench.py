@@ -19,10 +19,14 @@ roofline = the GEMV kernel: the timed graph holds only its launches, so its aver
 per call in a graph over >= 1 GiB of copies.
 measured_peak = HBM read and copy bandwidth over a 2 GiB buffer, by the reference's torch method and by the library's
 streaming probes; per_shape also gives each layer's share of the measured read peak.
-cpu_baseline = the reference's CPU path (oracle: dequantize to fp16, then torch.nn.functional.linear on the host) on a
-bounded sample of the same steps, plus the per-call breakdown at BASELINE configs[0] (quantize, dequantize + linear,
-linear alone; all torch threads and one).
+cpu_baseline = the reference's CPU torch path (its torch dequantize, lowbit/ops.py:119-123, restated in the oracle,
+then torch.nn.functional.linear; torch's CPU kernels on all their threads) on a bounded sample of the same steps, plus
+the per-call breakdown at BASELINE configs[0] (quantize, dequantize + linear, linear alone; all threads and one).
+skinny = the M = 2..64 half of the metric: us per call of the MFMA kernel (v5), dequantize + hipBLASLt and fp16
+hipBLASLt at M = 2, 16, 32, 64 on the 3B gate/up and 7B down shapes, with bandwidth and MFMA utilisation.
+provenance = GPU, software versions, source and library hashes and the dispatch constants of the run.
 """
+import hashlib
 import argparse
 import json
 import os
@@ -69,7 +73,17 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp16", action="store_true", help="skip the fp16 BLAS step")
-    ap.add_argument("--no-detail", action="store_true", help="skip the per-shape timings")
+    ap.add_argument("--no-detail", action="store_true",
+                    help="skip the measured peak, the per-shape timings and the skinny block (the timed graph only)")
+    ap.add_argument("--pmc-skinny", action="store_true",
+                    help="counter workload for the skinny path: a 1 GiB copy (calibration), then eager v5 calls at "
+                         "M = 16, 32, 64 on the 3B and 7B MLP shapes over cold copies")
+    ap.add_argument("--per-shape-only", action="store_true",
+                    help="profiler workload: only the per-shape graphs (the 8 BASELINE decode shapes and 7B gate/up "
+                         "and down), nothing else")
+    ap.add_argument("--replays", type=int, default=5,
+                    help="timed replays of the K-step graph: the first is the contract's timed region, all of them "
+                         "give the spread")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
     ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles"], default=None,
@@ -112,8 +126,9 @@ def build_pool(torch, ops, projs, gib=1.0, fp16=False, seed=0):
 
 
 def cpu_baseline(projs, host, xs, budget_s=15.0):
-    """The reference's CPU torch path on the host: dequantize (u - 8) * scale to fp16 (oracle,
-    reference lowbit/ops.py:119-123), then torch.nn.functional.linear -- timed over whole steps until budget_s."""
+    """The reference's CPU torch path on the host: its torch dequantize ((u - 8) * scale in fp32, rounded once to fp16,
+    reference lowbit/ops.py:119-123, restated as oracle.dequantize_w4_torch) then torch.nn.functional.linear, on all of
+    torch's threads -- timed over whole steps of the contract workload until budget_s."""
     import torch
     from oracle import quant_ref as R
     xh = {name: x.cpu() for name, x in xs.items()}
@@ -123,16 +138,16 @@ def cpu_baseline(projs, host, xs, budget_s=15.0):
         layer = host[steps % len(host)]
         for name, k, n in projs:
             packed, scales = layer[name]
-            w16 = torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP))
-            torch.nn.functional.linear(xh[name], w16)
+            R.cpu_torch_linear(xh[name], packed, scales, GROUP)
         steps += 1
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
     step_bytes = sum(alg_bytes(k, n) for _, k, n in projs)
     return {"value": round(step_bytes * steps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} steps of the same 14-projection M=1 sweep ({step_bytes / 1e6:.1f} MB each): oracle "
-                      f"dequant to fp16 + torch.nn.functional.linear on {threads} host threads, {el:.1f} s",
+            "sample": f"{steps} steps of the same 14-projection M=1 sweep ({step_bytes / 1e6:.1f} MB each): the "
+                      f"reference's torch dequantize to fp16 + torch.nn.functional.linear on {threads} host threads "
+                      f"(torch CPU kernels), {el:.1f} s",
             "ms_per_step": round(1000 * el / steps, 3), "config1": cpu_breakdown()}
 
 
@@ -148,9 +163,10 @@ def cpu_model():
 
 def cpu_breakdown(k=896, n=4864, rounds=5):
     """BASELINE configs[0] on the host: M=1, K=896, N=4864, weights N(0, 0.02), x N(0, 1) fp16, absmax g128. Median
-    seconds per call (after one warm-up) of (i) dequantize to fp16 + torch linear, (ii) torch linear on the
-    pre-dequantized fp16 weight, (iii) quantize (one-off), with torch on all its threads and on one; the oracle's
-    numpy steps are single-threaded either way. The fp64 error of the result is reported beside."""
+    milliseconds per call (after one warm-up) of (i) the reference's torch dequantize to fp16 + torch linear, (ii)
+    torch linear on the pre-dequantized fp16 weight, (iii) quantize (one-off; the reference's numpy quantizer, which
+    is single-threaded either way), with torch on all its threads and on one. The fp64 error of the result is
+    reported beside."""
     import numpy as np
     import torch
     from oracle import quant_ref as R
@@ -175,8 +191,8 @@ def cpu_breakdown(k=896, n=4864, rounds=5):
     for threads in (full, 1):
         torch.set_num_threads(threads)
         out[f"threads_{threads}"] = {
-            "dequant_linear_ms": med(lambda: torch.nn.functional.linear(
-                x, torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP)))),
+            "dequant_linear_ms": med(lambda: R.cpu_torch_linear(x, packed, scales, GROUP)),
+            "dequant_only_ms": med(lambda: R.dequantize_w4_torch(packed, scales, GROUP)),
             "linear_only_ms": med(lambda: torch.nn.functional.linear(x, w16)),
             "quantize_ms": med(lambda: R.quantize_w4(w, GROUP))}
     torch.set_num_threads(full)
@@ -278,6 +294,102 @@ def shape_detail(torch, ops, projs, pool, xs, peak=None):
     return out
 
 
+# the 7B-shaped MLP projections the per-shape table adds to the step's 1.5B / 3B shapes
+SHAPES_7B = [("7b.gate", 3584, 18944), ("7b.down", 18944, 3584)]
+# the skinny block of the default line: (name, K, N) x M (the M = 2..64 half of the metric)
+SKINNY_BLOCK = [("3b.gate_up", 2048, 11008), ("7b.down", 18944, 3584)]
+SKINNY_BLOCK_M = (2, 16, 32, 64)
+MFMA_F16_PEAK_TFLOPS = 2500.0               # MI355X dense fp16 MFMA
+
+
+def _sha256_files(paths):
+    h = hashlib.sha256()
+    for path in sorted(paths):
+        h.update(str(path.relative_to(ROOT)).encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def provenance(torch, ops):
+    """What the numbers were measured on and with (reference bench/gpu_run.py:41-66): GPU, driver-visible versions,
+    the source and library hashes, the git commit when the tree has one, and the dispatch constants."""
+    import subprocess
+    props = torch.cuda.get_device_properties(0)
+    pkg = ROOT / "lowbit-kernels_amd"
+    sources = [*(pkg / "csrc").glob("*"), *(pkg / "lowbit").glob("*.py"), *(ROOT / "include").glob("*.h"),
+               ROOT / "bench.py"]
+    lib = pkg / "lowbit" / "liblowbit_w4.so"
+    try:
+        commit = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "HEAD"], capture_output=True, text=True,
+                                timeout=10).stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        commit = None
+    return {"gpu": props.name, "gcn_arch": getattr(props, "gcnArchName", None), "cus": props.multi_processor_count,
+            "hbm_gib": round(props.total_memory / 2 ** 30, 1), "torch": torch.__version__,
+            "hip": getattr(torch.version, "hip", None), "git_commit": commit,
+            "sources_sha256": _sha256_files([q for q in sources if q.is_file()]),
+            "library_sha256": _sha256_files([lib]) if lib.exists() else None,
+            "library": ops._native.lib().lowbit_version().decode(),
+            "dispatch": {name: getattr(ops, name) for name in dir(ops) if name.startswith("AUTO_")},
+            "host": {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}}
+
+
+def skinny_block(torch, ops):
+    """The M = 2..64 half of the metric on the 3B gate/up and 7B down shapes: us per call of the
+    MFMA kernel (v5), dequantize + hipBLASLt and fp16 hipBLASLt, each a graph over >= 1 GiB of cold copies (int4 for
+    the first two, fp16 for the last); the v5 kernel's algorithmic bandwidth and its MFMA utilisation (2 M N K / t
+    against the 2.5 PFLOP/s dense fp16 peak)."""
+    rows = []
+    for name, k, n in SKINNY_BLOCK:
+        pool, pool16, _, copies = build_pool(torch, ops, [(name, k, n)], fp16=True, seed=k + n)
+        iters = max(200, copies)
+        for m in SKINNY_BLOCK_M:
+            x = torch.randn(m, k, device="cuda").half()
+            v5 = graph_time_us(torch, lambda i: ops.gemv(x, pool[i % copies][name], 5), iters)
+            dq = graph_time_us(torch, lambda i: torch.nn.functional.linear(x, ops.dequant(pool[i % copies][name],
+                                                                                            "mma")), iters)
+            f16 = graph_time_us(torch, lambda i: torch.nn.functional.linear(x, pool16[i % copies][name]), iters)
+            rows.append({"shape": name, "K": k, "N": n, "M": m, "mfma_v5_us": round(v5, 2),
+                         "dequant_hipblaslt_us": round(dq, 2), "fp16_hipblaslt_us": round(f16, 2),
+                         "v5_vs_dequant": round(dq / v5, 2), "v5_vs_fp16": round(f16 / v5, 2),
+                         "v5_GBps": round(alg_bytes(k, n, m) / (v5 * 1e-6) / 1e9, 1),
+                         "v5_mfma_util": round(2.0 * m * n * k / (v5 * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)})
+        del pool, pool16
+        torch.cuda.empty_cache()
+    return rows
+
+
+def per_shape_7b(torch, ops, peak=None):
+    """The 7B-shaped projections, per call like shape_detail, on one clip-searched weight cloned into >= 1 GiB."""
+    out = {}
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    for name, k, n in SHAPES_7B:
+        w = torch.randn(n, k, generator=gen, device="cuda") * 0.02
+        packed, scales = ops.quantize_w4_gpu(w, GROUP, CLIP_GRID)
+        base = ops.W4Weight(packed, scales, GROUP, ("mma",), device=packed.device)
+        del w
+        x = torch.randn(1, k, generator=gen, device="cuda").half()
+        out.update(shape_detail(torch, ops, [(name, k, n)], [{name: base}], {name: x}, peak))
+        del base, packed, scales
+        torch.cuda.empty_cache()
+    return out
+
+
+def per_shape_workload(a):
+    """Profiler workload: only the per-shape graphs (the 8 decode shapes of the step and the two 7B shapes), so a
+    kernel trace gives each shape's own GEMV duration (one grid size per shape)."""
+    import torch
+    from lowbit import ops
+    torch.cuda.set_device(0)
+    projs = step_projections()
+    pool, _, _, _ = build_pool(torch, ops, projs, gib=0.01)
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    xs = {name: torch.randn(1, k, generator=gen, device="cuda").half() for name, k, n in projs}
+    detail = shape_detail(torch, ops, projs, pool, xs)
+    detail.update(per_shape_7b(torch, ops))
+    print(json.dumps({"per_shape_workload": True, "per_shape": detail}), flush=True)
+
+
 def contract(a):
     import torch
     from lowbit import ops
@@ -320,12 +432,15 @@ def contract(a):
     graph.replay()                                   # one untimed replay: instantiation and first-touch costs
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    elapsed_ms = e0.elapsed_time(e1)
+    replay_ms = []
+    for _ in range(max(1, a.replays)):             # the first is the contract's timed region; the rest give the spread
+        torch.cuda.synchronize()
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        replay_ms.append(e0.elapsed_time(e1))
+    elapsed_ms = replay_ms[0]
     del graph
     launches = len(projs) * a.steps
     value = step_bytes * a.steps / (elapsed_ms / 1e3) / 1e9
@@ -340,6 +455,10 @@ def contract(a):
         fp16 = graph_time_us(torch, step16, a.steps, reps=1) / 1000
     peak = None if a.no_detail else measured_peak(torch, ops)
     detail = None if a.no_detail else shape_detail(torch, ops, projs, pool, xs, peak["read_gbps"])
+    if detail is not None:
+        detail.update(per_shape_7b(torch, ops, peak["read_gbps"]))
+    skinny = None if a.no_detail else skinny_block(torch, ops)
+    by_step = sorted(step_bytes / (t / a.steps / 1e3) / 1e9 for t in replay_ms)
 
     line = {
         "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1; us/call M=1..64 vs hipBLASLt fp16",
@@ -366,11 +485,16 @@ def contract(a):
                      "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false,CS>, CS = 1 / 2 / 4",
                      "kernel_avg_us": round(1000 * elapsed_ms / launches, 3), "launches": launches,
                      "bytes_per_launch_avg": step_bytes // len(projs)},
+        "replays": {"n": len(replay_ms), "ms_per_step": [round(t / a.steps, 4) for t in replay_ms],
+                    "GBps_median": round(by_step[len(by_step) // 2], 1), "GBps_min": round(by_step[0], 1),
+                    "GBps_max": round(by_step[-1], 1)},
         "fp16_blas_ms_per_step": round(fp16, 4) if fp16 else None,
         "speedup_vs_fp16_blas": round(fp16 / (elapsed_ms / a.steps), 3) if fp16 else None,
         "blas_backend": str(torch.backends.cuda.preferred_blas_library()),
         "measured_peak": peak,
         "per_shape": detail,
+        "skinny": skinny,
+        "provenance": provenance(torch, ops),
     }
     if peak:
         line["roofline"]["measured_peak_gbps"] = peak["read_gbps"]
@@ -574,6 +698,38 @@ def pmc_workload(a):
                       "step_bytes": sum(alg_bytes(k, n) for _, k, n in projs)}), flush=True)
 
 
+PMC_SKINNY_SHAPES = [("3b.gate_up", 2048, 11008), ("3b.down", 11008, 2048), ("7b.gate_up", 3584, 18944),
+                     ("7b.down", 18944, 3584)]
+PMC_SKINNY_M = (16, 32, 64)
+
+
+def pmc_skinny_workload(a):
+    """For rocprofv3 --pmc on the skinny path: one elementwise copy of exactly 1 GiB (the counters' calibration), then
+    per (shape, M) in PMC_SKINNY_SHAPES x PMC_SKINNY_M one eager MFMA GEMM (v5) call on each of C cold copies of the
+    weight (C covering >= 1 GiB), in that order; prints the order so a counter summary can attribute each dispatch."""
+    import torch
+    from lowbit import ops
+    torch.cuda.set_device(0)
+    src = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    order = []
+    for name, k, n in PMC_SKINNY_SHAPES:
+        copies = cloned_copies(torch, ops, k, n)
+        for m in PMC_SKINNY_M:
+            x = torch.randn(m, k, device="cuda").half()
+            for c in copies:
+                ops.gemv(x, c, 5)
+            order.append({"shape": name, "K": k, "N": n, "M": m, "launches": len(copies),
+                          "alg_bytes": alg_bytes(k, n, m), "flops": 2 * m * n * k})
+        torch.cuda.synchronize()
+        del copies
+        torch.cuda.empty_cache()
+    print(json.dumps({"pmc_skinny_workload": True, "kernel": "gemm_mfma", "order": order}), flush=True)
+
+
 # BASELINE configs 4 and 5: prompt length, greedy tokens, tokens per step of the teacher-forced feeds, clip search
 E2E = {"1.5b": dict(prompt=64, new=256, chunks=(1, 16, 48), feed=480, clip=False),
        "3b": dict(prompt=512, new=256, chunks=(1, 16, 48), feed=480, clip=True),
@@ -763,6 +919,10 @@ def main():
         sys.exit(2)
     if a.pmc_workload:
         pmc_workload(a)
+    elif a.pmc_skinny:
+        pmc_skinny_workload(a)
+    elif a.per_shape_only:
+        per_shape_workload(a)
     elif a.sweep == "skinny":
         sweep_skinny(a)
     elif a.sweep == "prefill":
