@@ -34,6 +34,39 @@ __device__ __forceinline__ void decode_word(uint32_t w, f16x2 p[4]) {
   p[3] = as_f16x2((w8 & 0x00F000F0u) | kMagic) * inv16 + m72;
 }
 
+// The decode's bit masks (scalar registers) and magic number (one vector register). gfx9 VOP3 instructions take no
+// literal operand and at most one scalar one, so with literal constants the compiler emits each (w & mask) | magic
+// as an AND and an OR; with the mask in an SGPR and the magic in a VGPR it is one v_and_or_b32, for one VGPR. Create
+// once per kernel, outside the loops (the empty asm hides the constants from constant folding).
+struct DecodeRegs {
+  uint32_t lo, hi, magic;
+};
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t in_sgpr(uint32_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+__device__ __forceinline__ DecodeRegs decode_regs() {
+  return DecodeRegs{in_sgpr(0x000F000Fu), in_sgpr(0x00F000F0u), in_vgpr(kMagic)};
+}
+
+// A v3 word as an MFMA A fragment: the eight fp16 values u - 8 (exact) for k0 .. k7 in k order, pairs as in
+// decode_word: four v_and_or_b32, two packed adds, two packed FMAs and one shift.
+__device__ __forceinline__ f16x8 decode_word_a(uint32_t w, const DecodeRegs& c) {
+  const f16x2 m1032 = {(f16)-1032.0f, (f16)-1032.0f};
+  const f16x2 m72 = {(f16)-72.0f, (f16)-72.0f};
+  const f16x2 inv16 = {(f16)0.0625f, (f16)0.0625f};
+  const uint32_t w8 = w >> 8;
+  const f16x2 p0 = as_f16x2((w & c.lo) | c.magic) + m1032;
+  const f16x2 p1 = as_f16x2((w & c.hi) | c.magic) * inv16 + m72;
+  const f16x2 p2 = as_f16x2((w8 & c.lo) | c.magic) + m1032;
+  const f16x2 p3 = as_f16x2((w8 & c.hi) | c.magic) * inv16 + m72;
+  return __builtin_bit_cast(f16x8, u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)});
+}
+
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
 
 // Subnormal decode for dot products: a nibble alone in the mantissa of an fp16 half (exponent 0) is the subnormal

@@ -8,12 +8,13 @@
 //   B (32 k x 16 activation rows): x[16 mt + r][128 c + 32 q + 8 j + 0..7], 16 bytes read from LDS.
 //   D: lane l holds rows n = 16 t + 4 q + v (v = 0..3) of column m = 16 mt + r.
 //
-// Decode: a nibble alone in bits 0..3 of an fp16 half is the exact subnormal u 2^-24 (fp16 denormals are on), so a
-// v3 word becomes the eight A values (pairs (k0,k1), (k2,k3), (k4,k5), (k6,k7)) with three shifts and four ANDs, and
-// every product u x 2^-24 is exact in fp32 whatever the magnitude of x. The offset 8 is removed per 128-k chunk by
-// subtracting the same MFMAs run on the constant "all nibbles 8": zero weights give exactly 0, and the rest is
-// sum((u - 8) x) 2^-24 accumulated in fp32. That chunk partial is multiplied by its rows' scales into the running
-// sums (2^24 is put back at the end).
+// Decode: each v3 word becomes the eight A values (pairs (k0,k1), (k2,k3), (k4,k5), (k6,k7)) u - 8, exact in fp16
+// (magic number, nine instructions per word with the constants in registers), so every product (u - 8) x is exact in
+// fp32 whatever the magnitude of x and zero weights give exactly 0. The four MFMAs of a 128-k chunk sum those products
+// in fp32; the chunk's sum is multiplied by its rows' fp32 group scales into the running sums (one FMA per output).
+// (An earlier decode put each nibble alone in an fp16 subnormal u 2^-24 and removed the offset 8 with a second set
+// of MFMAs on the constant "all nibbles 8": twice the MFMAs, and the per-chunk difference of two large sums
+// amplified fp32 rounding about 16-fold.)
 //
 // Workgroup: 4 x KS waves. Wave w owns RW 16-row tiles (tile-wave w % 4) in K-group w / 4; the K-groups split the
 // workgroup's 128-k chunks round-robin. The 4 waves of a K-group walk the same chunks, so each chunk of x is loaded
@@ -37,8 +38,6 @@ namespace {
 
 constexpr int kW = 4;              // waves per workgroup
 constexpr int kXPitch = 272;       // bytes per staged activation row (256 + 16: conflict-free 16-byte LDS reads)
-constexpr float kTwo24 = 16777216.0f;
-
 }  // namespace
 
 template <int MT, int RW, int D, int KS>
@@ -114,29 +113,23 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   for (int i = 0; i < RW; ++i)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const DecodeRegs dc = decode_regs();
 
-  const f16x8 a8 = __builtin_bit_cast(f16x8, u32x4{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
   auto consume = [&](int d, int b) {
-    f32x4 pt[RW][MT], xs[MT];
+    f32x4 pt[RW][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < RW; ++i)
 #pragma unroll
-      for (int i = 0; i < RW; ++i) pt[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int mt = 0; mt < MT; ++mt) pt[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       f16x8 bx[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+      for (int mt = 0; mt < MT; ++mt)
         bx[mt] = *reinterpret_cast<const f16x8*>(xbuf + b * kXBuf + (16 * mt + r) * kXPitch + 16 * (4 * q + j));
-        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, bx[mt], xs[mt], 0, 0, 0);
-      }
 #pragma unroll
       for (int i = 0; i < RW; ++i) {
-        const uint32_t wd = rw[d][i][j];
-        const f16x8 a = __builtin_bit_cast(
-            f16x8, u32x4{wd & 0x000F000Fu, (wd >> 4) & 0x000F000Fu, (wd >> 8) & 0x000F000Fu, (wd >> 12) & 0x000F000Fu});
+        const f16x8 a = decode_word_a(rw[d][i][j], dc);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) pt[i][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx[mt], pt[i][mt], 0, 0, 0);
       }
@@ -151,7 +144,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][mt][v] = fmaf(pt[i][mt][v] - xs[mt][v], sc[v], acc[i][mt][v]);
+        for (int v = 0; v < 4; ++v) acc[i][mt][v] = fmaf(pt[i][mt][v], sc[v], acc[i][mt][v]);
     }
   };
 
@@ -228,7 +221,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
-        const f32x4 v = acc[i][mt] * kTwo24;
+        const f32x4 v = acc[i][mt];
         if (epi.mode == kEpiSiluMul) {                      // up rows 8 + 4 q + v sit 32 lanes on (q + 2)
           const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
           if (q < 2 && m < M && n < N) store4_silu(m, n, v, up);
@@ -246,7 +239,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
     for (int mt = 0; mt < MT; ++mt) {
       const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
       if (kg > 0 || m >= M || n >= N) continue;
-      const f32x4 v = acc[i][mt] * kTwo24;
+      const f32x4 v = acc[i][mt];
       float* dst = mine + (size_t)m * N + n;
       if (vec) {
         *reinterpret_cast<f32x4*>(dst) = v;
@@ -349,22 +342,17 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const f16x8 a8 = __builtin_bit_cast(f16x8, u32x4{0x00080008u, 0x00080008u, 0x00080008u, 0x00080008u});
+  const DecodeRegs dc = decode_regs();
   auto consume = [&](int d) {
-    f32x4 pt[MT], xs[MT];
+    f32x4 pt[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) pt[mt] = xs[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) pt[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t wd = rw[d][j];
-      const f16x8 a = __builtin_bit_cast(
-          f16x8, u32x4{wd & 0x000F000Fu, (wd >> 4) & 0x000F000Fu, (wd >> 8) & 0x000F000Fu, (wd >> 12) & 0x000F000Fu});
+      const f16x8 a = decode_word_a(rw[d][j], dc);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const f16x8 bx = __builtin_bit_cast(f16x8, rx[d][mt][j]);
-        xs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a8, bx, xs[mt], 0, 0, 0);
-        pt[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bx, pt[mt], 0, 0, 0);
-      }
+      for (int mt = 0; mt < MT; ++mt)
+        pt[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, rx[d][mt][j]), pt[mt], 0, 0, 0);
     }
     const uint32_t sb = rs[d];
     const float sc[4] = {(float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<0>(sb)),
@@ -374,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[mt][v] = fmaf(pt[mt][v] - xs[mt][v], sc[v], acc[mt][v]);
+      for (int v = 0; v < 4; ++v) acc[mt][v] = fmaf(pt[mt][v], sc[v], acc[mt][v]);
   };
 
   // this wave's chunks are wave + j W, j < nj; full groups of D refill their slot D chunks ahead (past the end the
@@ -412,7 +400,7 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + r, n = n0 + 4 * q;
-    const f32x4 v = acc[mt] * kTwo24;
+    const f32x4 v = acc[mt];
     if (epi.mode == kEpiSiluMul) {                          // up rows 8 + 4 q + v sit 32 lanes on (q + 2)
       const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
       if (q < 2 && m < M && n < N) {
@@ -475,15 +463,25 @@ hipError_t dispatch_ring(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
   }
 }
 
-// one tile per workgroup, up to 8 waves (the register budget of 2 waves per SIMD): M <= 16 with a 4-deep ring, M <= 32
-// with 3 slots, M <= 64 with 2 (198 registers at M <= 48, 255 at M <= 64)
-template <int MT>
-hipError_t launch_tiles(const GemvArgs& a, int waves) {
-  constexpr int D = MT == 1 ? 4 : MT == 2 ? 3 : 2, kThreads = 512;
+// one tile per workgroup, up to 8 waves (the register budget of 2 waves per SIMD); ring slots as tiles_ring allows
+template <int MT, int D>
+hipError_t launch_tiles_d(const GemvArgs& a, int waves) {
+  constexpr int kThreads = 512;
   if (waves < 1 || 64 * waves > kThreads) return hipErrorInvalidConfiguration;   // never planned
   const size_t shmem = (size_t)(waves - 1) * MT * 64 * 16;
   return launch(gemm_mfma_tiles<MT, D, kThreads>, dim3((a.N + 15) / 16), dim3(64 * waves), shmem, a.stream, a.x, a.w,
                 a.s, a.y, a.M, a.N, a.K, a.G, a.epi);
+}
+
+template <int MT>
+hipError_t launch_tiles(const GemvArgs& a, int waves, int D) {
+  if constexpr (MT <= 2) {
+    if (D >= 4) return launch_tiles_d<MT, 4>(a, waves);
+  }
+  if constexpr (MT <= 3) {
+    if (D == 3) return launch_tiles_d<MT, 3>(a, waves);
+  }
+  return launch_tiles_d<MT, 2>(a, waves);
 }
 
 template <int MT>
@@ -504,12 +502,20 @@ hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 // or 3584 from 33 rows) and wide N keep row groups, which share the activations through LDS.
 bool tiles_win(int MT, int ntiles, int KC) { return MT <= 4 && ntiles <= 288 && KC * MT <= 64; }
 
+// deepest ring the one-tile kernel holds without spilling at 8 waves (hipcc -O3, gfx950: 112 / 186 / 204 registers at
+// MT = 1 / 2 / 3 with 4 / 4 / 3 slots; MT = 4 spills at 3 slots)
+int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
+
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
 // tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
 // N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
 // its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
 // split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
-// about kGemmTargetWaves waves run; a 3-slot ring for M <= 16 with up to two K-groups, else 2 slots.
+// about kGemmTargetWaves waves run (M <= 32; from 33 rows K-groups double only while the waves stay within
+// kGemmMaxWavesWide: 3B gate/up at M = 64 12.3 us with 2 K-groups against 13.5 with 4, 7B gate/up 28.4 with 1 against
+// 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP shapes at M = 48 and 64, while at M = 24..32
+// two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs 18.8 us at M = 24); a 3-slot ring for M <= 16
+// with up to two K-groups, else 2 slots.
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
   const GemvOverride o = gemv_override();
@@ -521,6 +527,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     waves = std::min(waves, 8);
     while (waves > 1 && waves > KC) waves /= 2;
     p.TW = waves;
+    p.D = (o.ring >= 2 && o.ring <= 4) ? std::min(o.ring, tiles_ring(p.MT)) : tiles_ring(p.MT);
     return p;
   }
   p.R = row_tiles >= 2 ? 2 : 1;
@@ -538,8 +545,10 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   int ks = 1;
   if (o.waves >= 4) {
     ks = o.waves / 4;
-  } else {
+  } else if (p.MT <= 2) {
     while (ks < 4 && (long)groups * S * kW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
+  } else {                                                  // from 33 rows: fewer, longer K-groups (see above)
+    while (ks < 4 && (long)groups * S * kW * 2 * ks <= kGemmMaxWavesWide && 2 * ks * S <= KC) ks *= 2;
   }
   while (ks > 1 && ks * S > KC) ks /= 2;
   p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);
@@ -566,8 +575,8 @@ hipError_t zero_words_launch(void* p, int n, hipStream_t stream) {
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
   const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
   if (p.TW > 0)
-    return p.MT == 1 ? launch_tiles<1>(a, p.TW) : p.MT == 2 ? launch_tiles<2>(a, p.TW)
-         : p.MT == 3 ? launch_tiles<3>(a, p.TW) : launch_tiles<4>(a, p.TW);
+    return p.MT == 1 ? launch_tiles<1>(a, p.TW, p.D) : p.MT == 2 ? launch_tiles<2>(a, p.TW, p.D)
+         : p.MT == 3 ? launch_tiles<3>(a, p.TW, p.D) : launch_tiles<4>(a, p.TW, p.D);
   uint32_t* ctr = static_cast<uint32_t*>(workspace);
   float* part = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kCounterBytes) : nullptr;
   switch (p.MT) {

@@ -116,6 +116,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
 
   const f16x2 m1032 = {(f16)-1032.0f, (f16)-1032.0f}, m72 = {(f16)-72.0f, (f16)-72.0f};
   const f16x2 inv16 = {(f16)0.0625f, (f16)0.0625f};
+  const DecodeRegs dc = decode_regs();                      // masks and magic in registers: v_and_or_b32
   // one chunk: the 16 A fragments (4 tiles x 4 k-steps) are decoded first; then per activation tile its 4 B
   // fragments are read and 16 MFMAs issued, so at most two tiles' B fragments are live
   auto consume = [&](int d, int b) {
@@ -127,10 +128,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
 #pragma unroll
       for (int st = 0; st < 4; ++st) {                      // (u - 8) exact, times the scale: one rounding
         const uint32_t wd = rw[d][i][st], w8 = wd >> 8;
-        const f16x2 p0 = (as_f16x2((wd & 0x000F000Fu) | kMagic) + m1032) * sc;
-        const f16x2 p1 = (as_f16x2((wd & 0x00F000F0u) | kMagic) * inv16 + m72) * sc;
-        const f16x2 p2 = (as_f16x2((w8 & 0x000F000Fu) | kMagic) + m1032) * sc;
-        const f16x2 p3 = (as_f16x2((w8 & 0x00F000F0u) | kMagic) * inv16 + m72) * sc;
+        const f16x2 p0 = (as_f16x2((wd & dc.lo) | dc.magic) + m1032) * sc;
+        const f16x2 p1 = (as_f16x2((wd & dc.hi) | dc.magic) * inv16 + m72) * sc;
+        const f16x2 p2 = (as_f16x2((w8 & dc.lo) | dc.magic) + m1032) * sc;
+        const f16x2 p3 = (as_f16x2((w8 & dc.hi) | dc.magic) * inv16 + m72) * sc;
         a[i][st] = __builtin_bit_cast(f16x8, u32x4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)});
       }
     }

@@ -85,6 +85,7 @@ constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many byte
 // counters (zero before first use, left zero by every launch), followed by the fp32 partial sums [splits][M][N].
 constexpr int kGemmMaxGroups = 320;
 constexpr int kGemmTargetWaves = 1792;
+constexpr int kGemmMaxWavesWide = 2048;
 // prefill GEMM: K is split while the work items fill fewer than two rounds of this many workgroups
 constexpr int kPrefillTargetGroups = 256;
 // decode attention: when the cache holds at least kAttnMinSplitKeys keys, keys are split across blocks while
@@ -97,13 +98,12 @@ constexpr int kAttnManyBlocks = 512;      // from this many blocks on, at most 4
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
 // (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
-// register budget of 4 KS waves per workgroup without spilling (hipcc -O3), and the LDS of the K-groups' x buffers
+// register budget of 4 KS waves per workgroup without spilling (hipcc -O3, gfx950: 128 registers at 4 K-groups, 256 at
+// 2), and the LDS of the K-groups' x buffers
 constexpr bool gemm_fits(int MT, int RW, int D, int KS) {
-  if (KS == 4) return (MT == 1 && RW == 1 && D <= 3) || (MT == 1 && RW == 2 && D == 2) || (MT == 2 && RW == 1 && D == 2);
-  if (KS == 2)
-    return MT == 1 || (MT == 2 && (RW == 1 || D <= 3)) || (MT == 3 && (RW == 1 ? D <= 3 : D == 2)) ||
-           (MT == 4 && D == 2);
-  return !(MT == 4 && RW == 2 && D == 4);
+  if (KS == 4) return D == 2 ? (RW == 1 ? MT <= 3 : MT <= 2) : (RW == 1 && MT == 1);
+  if (KS == 2) return !((RW == 2 && (MT >= 3 ? D >= 3 : (MT == 2 && D == 4))) || (MT == 4 && RW == 1 && D == 4));
+  return true;
 }
 constexpr int kMaxGroups = 2048;         // K / G limit of the MFMA-layout GEMV (scales staged in LDS)
 constexpr int64_t kMaxK = 1 << 22;       // K limit of the MFMA-layout kernels (32-bit buffer offsets)
