@@ -1,9 +1,17 @@
-"""Build liblowbit_w4.so (gfx950 only) in-tree: lowbit-kernels_amd/lowbit/liblowbit_w4.so.
+"""Build the libraries in-tree (gfx950 only):
+
+    lowbit-kernels_amd/lowbit/liblowbit_w4.so      every kernel and the C ABI (hipcc)
+    lowbit-kernels_amd/lowbit/liblowbit_format.so  the host format functions alone (g++; no HIP dependency), which
+                                                   lowbit.quant loads, so packing weights needs no GPU stack
 
     python lowbit-kernels_amd/build.py [--jobs N] [--asm]
+    python lowbit-kernels_amd/build.py --sanitize   # CPU ASan + UBSan build of the host code into _build_asan/
 
-Every source is compiled with hipcc for gfx950 (host code for the .cpp file), in parallel, then linked. --asm also
-writes the device assembly of each kernel file into lowbit-kernels_amd/_build/ for inspection.
+Every source is compiled with hipcc for gfx950 (host code for the .cpp files), in parallel, then linked. --asm also
+writes the device assembly of each kernel file into lowbit-kernels_amd/_build/ for inspection. --sanitize builds the
+host code (the format functions, the C ABI's validation, the launch planners) with AddressSanitizer and
+UndefinedBehaviorSanitizer -- the device code is built without them -- into _build_asan/liblowbit_w4.so and
+_build_asan/liblowbit_format.so, then runs tests/test_quant.py and tests/test_capi.py against them (no GPU needed).
 """
 import argparse
 import concurrent.futures as cf
@@ -18,8 +26,15 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 OUT = PKG / "lowbit" / "liblowbit_w4.so"
+OUT_FORMAT = PKG / "lowbit" / "liblowbit_format.so"
+ASAN = PKG / "_build_asan"
 SOURCES = ["capi.hip", "gemv.hip", "gemm_mfma.hip", "gemm_prefill.hip", "dequant.hip", "quantize.hip", "decode_ops.hip", "hbm_probe.hip",
-           "host_format.cpp"]
+           "host_format.cpp", "status.cpp"]
+FORMAT_SOURCES = ["host_format.cpp", "status.cpp"]
+# host-only sanitizers: on a hipcc line each -fsanitize= goes after -Xarch_host, so the device code is built without
+SANITIZE_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined", "-Xarch_host",
+                 "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+
 ARCH = "gfx950"
 # packed-fp32 ops stay off: only scalar fp32 and packed fp16 arithmetic is emitted
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
@@ -39,12 +54,13 @@ def _run(cmd):
     return p.returncode, err
 
 
-def compile_one(src, asm=False):
-    obj = BUILD / (src + ".o")
+def compile_one(src, asm=False, outdir=BUILD, extra=()):
+    obj = outdir / (src + ".o")
     if src.endswith(".hip"):
-        cmd = [hipcc(), f"--offload-arch={ARCH}", "-x", "hip", *COMMON, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-x", "hip", *COMMON, *DEVICE_FLAGS, *extra, "-c", str(CSRC / src),
+               "-o", str(obj)]
     else:
-        cmd = [hipcc(), *COMMON, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [hipcc(), *COMMON, *extra, "-c", str(CSRC / src), "-o", str(obj)]
     rc, err = _run(cmd)
     if rc:
         return src, rc, err
@@ -56,24 +72,55 @@ def compile_one(src, asm=False):
     return src, 0, err
 
 
-def build(jobs=None, asm=False, verbose=False):
-    BUILD.mkdir(exist_ok=True)
+def build_format(out=OUT_FORMAT, extra=(), compiler="g++"):
+    """The host format functions alone, with g++ (hipcc's host compiler for the sanitizer build, so that one ASan
+    runtime serves both libraries): no HIP runtime dependency."""
+    tmp = out.with_suffix(".so.tmp")
+    rc, err = _run([compiler, "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-Wall", f"-I{ROOT / 'include'}",
+                    f"-I{CSRC}", *extra, *[str(CSRC / src) for src in FORMAT_SOURCES], "-o", str(tmp)])
+    if rc:
+        raise RuntimeError(f"g++ failed on the format library:\n{err}")
+    os.replace(tmp, out)
+    return out
+
+
+def build(jobs=None, asm=False, verbose=False, outdir=BUILD, out=OUT, extra=()):
+    outdir.mkdir(exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(jobs) as ex:
-        results = list(ex.map(lambda s: compile_one(s, asm), SOURCES))
+        results = list(ex.map(lambda s: compile_one(s, asm, outdir, extra), SOURCES))
     failed = [(s, err) for s, rc, err in results if rc]
     for s, rc, err in results:
         if err.strip() and (verbose or rc):
             print(f"--- {s}\n{err}", file=sys.stderr)
     if failed:
         raise RuntimeError(f"hipcc failed on {[s for s, _ in failed]}")
-    tmp = OUT.with_suffix(".so.tmp")
-    rc, err = _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
-                    *[str(BUILD / (s + ".o")) for s in SOURCES]])
+    tmp = out.with_suffix(".so.tmp")
+    rc, err = _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *extra, "-o", str(tmp),
+                    *[str(outdir / (s + ".o")) for s in SOURCES]])
     if rc:
         raise RuntimeError(f"link failed:\n{err}")
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    if out == OUT:
+        build_format()
+    return out
+
+
+def sanitizer_check(jobs=None):
+    """Build the host code with ASan + UBSan and run the CPU tests of the format functions and the C ABI on it."""
+    ASAN.mkdir(exist_ok=True)
+    lib = build(jobs, outdir=ASAN, out=ASAN / "liblowbit_w4.so", extra=SANITIZE_HOST)
+    fmt = build_format(ASAN / "liblowbit_format.so", SANITIZE_HOST, compiler=hipcc())
+    # python itself is not instrumented: clang's ASan runtime is preloaded
+    clang_rt = subprocess.run([hipcc(), "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True,
+                              text=True).stdout.strip()
+    env = dict(os.environ, LOWBIT_LIB=str(lib), LOWBIT_FORMAT_LIB=str(fmt), LD_PRELOAD=clang_rt,
+               ASAN_OPTIONS="detect_leaks=0:halt_on_error=1", UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
+    tests = [str(ROOT / "tests" / "test_quant.py"), str(ROOT / "tests" / "test_capi.py")]
+    p = subprocess.run([sys.executable, "-m", "pytest", "-q", "-p", "no:cacheprovider", *tests], env=env, text=True,
+                       capture_output=True)
+    print(p.stdout[-3000:], p.stderr[-3000:], sep="\n")
+    return p.returncode
 
 
 def main():
@@ -81,7 +128,10 @@ def main():
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--asm", action="store_true")
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--sanitize", action="store_true", help="ASan + UBSan build of the host code, then its CPU tests")
     a = ap.parse_args()
+    if a.sanitize:
+        sys.exit(sanitizer_check(a.jobs))
     print(build(a.jobs, a.asm, a.verbose))
 
 

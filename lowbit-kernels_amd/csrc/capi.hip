@@ -12,11 +12,6 @@
 
 namespace lowbit {
 
-char* error_buffer() {
-  static thread_local char buf[512];
-  return buf;
-}
-
 namespace {
 
 constexpr int kMaxDevices = 64;
@@ -184,25 +179,6 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
 using namespace lowbit;
 
 extern "C" {
-
-const char* lowbit_last_error(void) { return error_buffer(); }
-
-const char* lowbit_strerror(int status) {
-  switch (status) {
-    case LOWBIT_OK: return "ok";
-    case LOWBIT_ERR_ARG: return "invalid argument";
-    case LOWBIT_ERR_GROUP: return "invalid group size";
-    case LOWBIT_ERR_SHAPE: return "shape mismatch";
-    case LOWBIT_ERR_ALIGN: return "misaligned pointer";
-    case LOWBIT_ERR_ROWS: return "row count out of range";
-    case LOWBIT_ERR_VERSION: return "unknown kernel version";
-    case LOWBIT_ERR_LAYOUT: return "layout needs K and G multiples of 128";
-    case LOWBIT_ERR_TUNING: return "invalid tuning knob";
-    case LOWBIT_ERR_HIP: return "HIP error";
-    case LOWBIT_ERR_DEVICE: return "unsupported device";
-    default: return "unknown status";
-  }
-}
 
 const char* lowbit_version(void) { return "lowbit_w4 0.1 gfx950"; }
 

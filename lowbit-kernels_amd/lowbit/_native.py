@@ -12,12 +12,15 @@ import pathlib
 
 LIB_NAME = "liblowbit_w4.so"
 LIB_PATH = pathlib.Path(__file__).resolve().parent / LIB_NAME
+# the host format functions alone (lowbit_host_*, lowbit_last_error, lowbit_strerror), built with g++: no HIP
+FORMAT_LIB_PATH = pathlib.Path(__file__).resolve().parent / "liblowbit_format.so"
 
 LAYOUT_CANONICAL, LAYOUT_V3, LAYOUT_MFMA, LAYOUT_NV_MMA = 0, 1, 2, 3
 EPI_STORE, EPI_BIAS, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2, 3
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _LIB = None
+_FORMAT_LIB = None
 
 _i64, _int, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
 SIGNATURES = {
@@ -68,10 +71,31 @@ def lib():
     return _LIB
 
 
-def check(rc):
-    """Raise RuntimeError with the library's message for a non-zero status."""
+HOST_FUNCTIONS = ("lowbit_last_error", "lowbit_strerror", "lowbit_host_quantize", "lowbit_host_unpack",
+                  "lowbit_host_dequantize", "lowbit_host_relayout", "lowbit_host_gemv_reference")
+
+
+def host_lib():
+    """The HIP-free host format library (loaded once), which lowbit.quant uses: packing weights needs no GPU stack.
+    Raises RuntimeError if it has not been built."""
+    global _FORMAT_LIB
+    if _FORMAT_LIB is None:
+        path = pathlib.Path(os.environ.get("LOWBIT_FORMAT_LIB", FORMAT_LIB_PATH))
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built: run `python lowbit-kernels_amd/build.py`")
+        handle = ctypes.CDLL(str(path))
+        for name in HOST_FUNCTIONS:
+            fn = getattr(handle, name)
+            fn.argtypes, fn.restype = SIGNATURES[name]
+        _FORMAT_LIB = handle
+    return _FORMAT_LIB
+
+
+def check(rc, library=None):
+    """Raise RuntimeError with the library's message for a non-zero status (`library`: the one that returned it,
+    the kernel library by default)."""
     if rc != 0:
-        l = lib()
+        l = library if library is not None else lib()
         msg = l.lowbit_last_error().decode() or l.lowbit_strerror(rc).decode()
         raise RuntimeError(msg)
 

@@ -1,5 +1,6 @@
 """Weight-only INT4 format: the public host-side functions of the reference's lowbit/quant.py, same names and
-semantics, computed by the native library's host code (liblowbit_w4.so, lowbit_host_*), bit for bit.
+semantics, computed by the native library's host code (lowbit_host_* in liblowbit_format.so, a HIP-free build of
+the same functions liblowbit_w4.so exports), bit for bit. No GPU stack is needed to pack weights.
 
 Format (reference lowbit/quant.py:1-17): for an nn.Linear weight W [N, K], one fp16 scale per group of G values
 along K, scale = fp16(max|W_group| / 7) (an all-zero group gets 1.0), q = clamp(round_half_even(W / scale), -8, 7),
@@ -24,6 +25,10 @@ SLOT_TO_K = np.array([0, 2, 4, 6, 1, 3, 5, 7])
 MMA_BYTE_ORDER = np.array([4 * s + t for t in range(4) for s in range(16)])
 
 
+def _check(rc):
+    _native.check(rc, _native.host_lib())
+
+
 def _u8(packed):
     return np.ascontiguousarray(np.asarray(packed, dtype=np.uint8))
 
@@ -38,7 +43,7 @@ def quantize_w4(w, group=128):
         raise ValueError(f"K={k} must be a multiple of the group size {group}, itself a multiple of 32")
     packed = np.empty((n, k // 2), dtype=np.uint8)
     scales = np.empty((n, k // group), dtype=np.float16)
-    _native.check(_native.lib().lowbit_host_quantize(_native.np_ptr(w), _native.np_ptr(packed), _native.np_ptr(scales),
+    _check(_native.host_lib().lowbit_host_quantize(_native.np_ptr(w), _native.np_ptr(packed), _native.np_ptr(scales),
                                                      n, k, group))
     return packed, scales
 
@@ -47,7 +52,7 @@ def unpack_w4(packed):
     """packed uint8 [N, K//2] -> signed int8 values [N, K] in -8..7."""
     packed = _u8(packed)
     out = np.empty((packed.shape[0], packed.shape[1] * 2), dtype=np.int8)
-    _native.check(_native.lib().lowbit_host_unpack(_native.np_ptr(packed), _native.np_ptr(out), packed.shape[0],
+    _check(_native.host_lib().lowbit_host_unpack(_native.np_ptr(packed), _native.np_ptr(out), packed.shape[0],
                                                    packed.shape[1] * 2))
     return out
 
@@ -58,7 +63,7 @@ def dequantize_w4(packed, scales, group=128):
     scales = np.ascontiguousarray(np.asarray(scales, dtype=np.float16))
     n, k = packed.shape[0], packed.shape[1] * 2
     out = np.empty((n, k), dtype=np.float32)
-    _native.check(_native.lib().lowbit_host_dequantize(_native.np_ptr(packed), _native.np_ptr(scales),
+    _check(_native.host_lib().lowbit_host_dequantize(_native.np_ptr(packed), _native.np_ptr(scales),
                                                        _native.np_ptr(out), n, k, group))
     return out
 
@@ -66,7 +71,7 @@ def dequantize_w4(packed, scales, group=128):
 def _relayout(packed, layout):
     packed = _u8(packed)
     out = np.empty_like(packed)
-    _native.check(_native.lib().lowbit_host_relayout(_native.np_ptr(packed), _native.np_ptr(out), packed.shape[0],
+    _check(_native.host_lib().lowbit_host_relayout(_native.np_ptr(packed), _native.np_ptr(out), packed.shape[0],
                                                      packed.shape[1] * 2, layout))
     return out
 
@@ -104,6 +109,6 @@ def gemv_reference(x, packed, scales, group=128):
     if packed.shape[1] * 2 != k:
         raise ValueError("x [M, K] and packed [N, K/2] disagree on K")
     y = np.empty((m, n), dtype=np.float64)
-    _native.check(_native.lib().lowbit_host_gemv_reference(_native.np_ptr(x), _native.np_ptr(packed),
+    _check(_native.host_lib().lowbit_host_gemv_reference(_native.np_ptr(x), _native.np_ptr(packed),
                                                            _native.np_ptr(scales), _native.np_ptr(y), m, n, k, group))
     return y

@@ -96,3 +96,33 @@ def test_check_raises_runtime_error_with_the_message():
     lib.lowbit_w4_gemv(FAKE, FAKE, FAKE, FAKE, 9, 16, 128, 128, 6, 0, None)
     with pytest.raises(RuntimeError, match="1..8 rows"):
         _native.check(5)
+
+
+def test_format_library_needs_no_gpu_stack():
+    """liblowbit_format.so (the host format functions, built with g++) exports them with the same error reporting and
+    links no HIP library, so lowbit.quant packs weights on a machine without ROCm."""
+    import shutil
+    import subprocess
+    host = _native.host_lib()
+    for name in _native.HOST_FUNCTIONS:
+        assert hasattr(host, name), name
+    assert host.lowbit_host_unpack(None, None, 1, 32) == 1 and b"null" in host.lowbit_last_error()
+    if shutil.which("readelf"):
+        needed = subprocess.run(["readelf", "-d", str(_native.FORMAT_LIB_PATH)], capture_output=True, text=True).stdout
+        assert "NEEDED" in needed and "amdhip" not in needed and "hsa" not in needed
+
+
+def test_quant_runs_without_the_kernel_library(tmp_path):
+    """With the kernel library unreachable (LOWBIT_LIB points nowhere), lowbit.quant still quantizes and relayouts."""
+    import os
+    import subprocess
+    import sys
+    code = ("import numpy as np; from lowbit import quant; "
+            "p, s = quant.quantize_w4(np.ones((2, 128), np.float32)); "
+            "assert p[0, 0] == 0xFF and float(s[0, 0]) == np.float16(1 / 7); "
+            "assert quant.interleave_for_mfma(p).shape == (2, 64); print('ok')")
+    root = pathlib.Path(__file__).resolve().parent.parent
+    env = dict(os.environ, LOWBIT_LIB=str(tmp_path / "missing.so"),
+               PYTHONPATH=os.pathsep.join([str(root / "lowbit-kernels_amd"), str(root)]))
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.strip() == "ok", out.stderr[-2000:]

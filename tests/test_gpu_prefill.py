@@ -152,3 +152,18 @@ def test_prefill_group_sizes(cuda, k, n, m, g):
     ref = x.double() @ ref_w.t()
     assert rel(y, ref) < bound(x, ref_w, ref)
     assert_rounds(y, x.double() @ ops.dequant(wq, "mma").double().t())
+
+
+@pytest.mark.parametrize("k,n,m", [(2048, 2560, 130), (11008, 2048, 130), (896, 4864, 64)])
+def test_gemm_chunked_is_v5_in_64_row_slices(cuda, k, n, m):
+    """ops.gemm_chunked (reference lowbit/ops.py:145-148): many rows through the MFMA kernel 64 at a time, with no fp16
+    weight copy; the same bits as the v5 kernel on each slice, and within the fp64 bound."""
+    wq, ref_w, *_, gen = make_weight(k, n, 3 * k + n, layouts=("mma",), sd=0.02)
+    x = torch.randn(m, k, generator=gen).half().cuda()
+    y = ops.gemm_chunked(x, wq)
+    assert tuple(y.shape) == (m, n)
+    slices = torch.cat([ops.gemv(x[i:i + 64].contiguous(), wq, 5) for i in range(0, m, 64)])
+    assert torch.equal(y, slices)
+    ref = x.double() @ ref_w.T
+    assert rel(y, ref) <= bound(x, ref_w, ref)
+    assert_rounds(y, ref)
