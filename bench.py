@@ -86,9 +86,10 @@ def parse():
                          "give the spread")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles"], default=None,
+    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles", "tilewaves"], default=None,
                     help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
-                         "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32")
+                         "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32; "
+                         "tilewaves: the row groups' tile-waves per K-group on layers past 1024 tiles")
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
@@ -636,6 +637,43 @@ def sweep_tiles(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+def sweep_tilewaves(a):
+    """MFMA GEMM (v5) row groups on the layers past 1024 tiles (and two at or below it), M in {16, 32, 48, 64}:
+    graph-timed us per call of the automatic plan, of 4 tile-waves per K-group (lowbit_set_gemm_tile_waves(4), the
+    rest automatic) and of 5, 6 and 8 tile-waves with 1 or 2 K-groups."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in ((3584, 18944), (2048, 22016), (1536, 17920), (3584, 37888), (2048, 11008), (3584, 16384)):
+        cl = cloned_copies(torch, ops, k, n)
+        for m in (16, 32, 48, 64):
+            x = torch.randn(m, k, device="cuda").half()
+            t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5), max(400, len(cl))), 2)
+            r = {"K": k, "N": n, "M": m, "auto": t()}
+            try:
+                _native.check(lib.lowbit_set_gemm_tile_waves(4))
+                r["tw4"] = t()
+                for tw in (5, 6, 8):
+                    for ks in (1, 2):
+                        if tw * ks > 12 and m > 48:            # never built (register budget)
+                            continue
+                        _native.check(lib.lowbit_set_gemm_tile_waves(tw))
+                        _native.check(lib.lowbit_set_launch_override(4 * ks, 0, 0))
+                        r[f"tw{tw}_kg{ks}"] = t()
+                        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+            finally:
+                _native.check(lib.lowbit_set_gemm_tile_waves(0))
+                _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+            rows.append(r)
+            print(json.dumps(r), flush=True)
+        del cl
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
 def sweep_prefill(a):
     """Prefill, M in {128, 256, 512, 2048} on the Qwen2.5-3B layer (merged q|k|v and gate|up, o, down) and the 7B MLP
     projections: us/call of dequantize + hipBLASLt, fp16 hipBLASLt, the int4 prefill GEMM (automatic launch plan), the
@@ -931,6 +969,8 @@ def main():
         sweep_gemv(a)
     elif a.sweep == "tiles":
         sweep_tiles(a)
+    elif a.sweep == "tilewaves":
+        sweep_tilewaves(a)
     elif a.e2e and a.decode_trace:
         decode_trace(a)
     elif a.e2e:

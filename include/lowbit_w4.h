@@ -73,6 +73,12 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
  * counterpart in the reference. */
 int lowbit_set_gemm_kernel(int kernel);
 
+/* Process-wide choice of the MFMA GEMM's tile-waves per K-group in its row-group structure, for tuning sweeps and
+ * tests: 0 = automatic; 4, 5, 6 or 8 (5, 6 and 8 with one 16-row tile per wave, 2 ring slots and at most 2 K-groups;
+ * with row_tiles = 2 the GEMM keeps 4). Each tile is computed the same way whatever the count, so the results are
+ * identical bit for bit. Affects later launches only. No counterpart in the reference. */
+int lowbit_set_gemm_tile_waves(int tile_waves);
+
 /* y[M, N] (fp16) = x[M, K] (fp16) . dequant(W)^T, 1 <= M <= 8.
  * Replaces the reference's w4_gemv (csrc/w4_gemv.cu:454-484) and, through it, ops.gemv(version in 1..4, 6)
  * (lowbit/ops.py:67-78). version 1 or 2: w in the canonical layout; 3 or 4: v3 layout; 6: the MFMA layout (needs

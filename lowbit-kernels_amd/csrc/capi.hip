@@ -34,7 +34,8 @@ int check_device() {
   return LOWBIT_OK;
 }
 
-std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0}, g_override_gemm{0};
+std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0}, g_override_gemm{0},
+    g_override_tile_waves{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -118,6 +119,7 @@ GemvOverride gemv_override() {
   o.ring = g_override_ring.load(std::memory_order_relaxed);
   o.splits = g_override_splits.load(std::memory_order_relaxed);
   o.gemm_kernel = g_override_gemm.load(std::memory_order_relaxed);
+  o.tile_waves = g_override_tile_waves.load(std::memory_order_relaxed);
   return o;
 }
 
@@ -198,6 +200,13 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
 int lowbit_set_gemm_kernel(int kernel) {
   if (kernel < 0 || kernel > 2) return fail(LOWBIT_ERR_TUNING, "kernel is 0 (auto), 1 (row groups) or 2 (one tile each)");
   g_override_gemm.store(kernel, std::memory_order_relaxed);
+  return ok();
+}
+
+int lowbit_set_gemm_tile_waves(int tile_waves) {
+  if (!(tile_waves == 0 || tile_waves == 4 || tile_waves == 5 || tile_waves == 6 || tile_waves == 8))
+    return fail(LOWBIT_ERR_TUNING, "tile_waves is 0 (auto), 4, 5, 6 or 8");
+  g_override_tile_waves.store(tile_waves, std::memory_order_relaxed);
   return ok();
 }
 

@@ -36,23 +36,28 @@ namespace lowbit {
 
 namespace {
 
-constexpr int kW = 4;              // waves per workgroup
+constexpr int kW = 4;              // tile-waves per K-group of the default shape
 constexpr int kXPitch = 272;       // bytes per staged activation row (256 + 16: conflict-free 16-byte LDS reads)
 }  // namespace
 
-template <int MT, int RW, int D, int KS>
-__global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+template <int MT, int RW, int D, int KS, int TW>
+__global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                       const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                       int S, uint32_t* __restrict__ ctr, float* __restrict__ part,
                                                       Epilogue epi) {
-  constexpr int T = kW * RW;                               // 16-row tiles per workgroup
+  constexpr int T = TW * RW;                               // 16-row tiles per workgroup
   constexpr int kXBuf = 16 * MT * kXPitch;                 // one staged chunk of x
+  // a chunk of x is 16 MT rows x 16 pieces of 16 bytes, staged by the 64 TW threads of a K-group, kPer pieces each
+  constexpr int kPieces = 16 * 16 * MT, kGroupThreads = 64 * TW;
+  constexpr int kPer = (kPieces + kGroupThreads - 1) / kGroupThreads;
+  constexpr bool kWhole = kPieces % kGroupThreads == 0;    // else the last round of pieces is partial
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_last;
   args_in_sgprs(x, w, s, y, M, N, K, G, S, ctr, part, epi.aux);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = wave >> 2, tw = wave & 3, gt = tid & 255;  // K-group, tile-wave, thread index inside the K-group
+  const int kg = wave / TW, tw = wave - kg * TW;            // K-group, tile-wave
+  const int gt = tid - kGroupThreads * kg;                  // thread index inside the K-group
   const int r = lane & 15, q = lane >> 4;
   const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
   const int grp = blockIdx.x, split = blockIdx.y;
@@ -78,11 +83,19 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
   }
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)N * (uint32_t)KG * 2u);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
-  int xoff[MT];                                              // this thread's x pieces: row gt / 16 + 16 u
+  // this thread's x pieces: piece pc = gt + 64 TW u is row pc / 16, bytes 16 (pc % 16) of the chunk; rows >= M read
+  // past the end (zeros); in a partial last round, threads past the last piece (xl < 0) load and store nothing
+  int xoff[kPer], xl[kPer];
 #pragma unroll
-  for (int u = 0; u < MT; ++u) xoff[u] = (((gt >> 4) + 16 * u) * K + 8 * (gt & 15)) * 2;   // rows >= M: past the end
+  for (int u = 0; u < kPer; ++u) {
+    const int pc = gt + kGroupThreads * u;
+    const bool in = kWhole || pc < kPieces;
+    xoff[u] = in ? ((pc >> 4) * K + 8 * (pc & 15)) * 2 : kOutOfRange;
+    xl[u] = in ? (pc >> 4) * kXPitch + 16 * (pc & 15) : -1;
+  }
+  auto piece_live = [&](int u) { return kWhole || u + 1 < kPer || xl[u] >= 0; };
 
-  u32x4 rw[D][RW], rx[D][MT];
+  u32x4 rw[D][RW], rx[D][kPer];
   uint32_t rs[D][RW];
   const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
   auto issue = [&](int d, int step) {
@@ -95,12 +108,12 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
       rs[d][i] = buffer_load2(sr, live ? soff[i] + 2 * g : kOutOfRange);
     }
 #pragma unroll
-    for (int u = 0; u < MT; ++u) rx[d][u] = buffer_load16(xr, live ? xoff[u] + 256 * c : kOutOfRange);
+    for (int u = 0; u < kPer; ++u) rx[d][u] = buffer_load16(xr, live && piece_live(u) ? xoff[u] + 256 * c : kOutOfRange);
   };
   auto stage_x = [&](int d, int b) {                        // x pieces of slot d -> LDS buffer b
 #pragma unroll
-    for (int u = 0; u < MT; ++u)
-      *reinterpret_cast<u32x4*>(xbuf + b * kXBuf + ((gt >> 4) + 16 * u) * kXPitch + 16 * (gt & 15)) = rx[d][u];
+    for (int u = 0; u < kPer; ++u)
+      if (piece_live(u)) *reinterpret_cast<u32x4*>(xbuf + b * kXBuf + xl[u]) = rx[d][u];
   };
 
 #pragma unroll
@@ -179,7 +192,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 #pragma unroll
       for (int i = 0; i < RW; ++i)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) red[((((kg - 1) * kW + tw) * RW + i) * MT + mt) * 64 + lane] = acc[i][mt];
+        for (int mt = 0; mt < MT; ++mt) red[((((kg - 1) * TW + tw) * RW + i) * MT + mt) * 64 + lane] = acc[i][mt];
     }
     __syncthreads();
     if (kg == 0) {
@@ -188,7 +201,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
 #pragma unroll
         for (int i = 0; i < RW; ++i)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[i][mt] += red[((((g2 - 1) * kW + tw) * RW + i) * MT + mt) * 64 + lane];
+          for (int mt = 0; mt < MT; ++mt) acc[i][mt] += red[((((g2 - 1) * TW + tw) * RW + i) * MT + mt) * 64 + lane];
     }
   }
 
@@ -275,7 +288,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_mfma(const f16* __restrict__ x,
     }
     return sum;
   };
-  for (int it = tid; it < M * nq; it += 256 * KS) {
+  for (int it = tid; it < M * nq; it += kGroupThreads * KS) {
     const int m = it / nq, n = n0 + 4 * (it - m * nq);
     if (epi.mode == kEpiSiluMul) {
       if ((n & 15) < 8) store4_silu(m, n, split_sum(m, n), split_sum(m, n + 8));
@@ -426,22 +439,33 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
 
 namespace {
 
-template <int MT, int RW, int D, int KS>
+template <int MT, int RW, int D, int KS, int TW = kW>
 hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
-  if constexpr (!gemm_fits(MT, RW, D, KS)) {
+  if constexpr (!gemm_fits(MT, RW, D, KS, TW)) {
     return hipErrorInvalidConfiguration;                    // never planned
   } else {
-    const int ntiles = (a.N + 15) / 16, groups = (ntiles + kW * RW - 1) / (kW * RW);
-    const size_t xbytes = (size_t)KS * 2 * 16 * MT * kXPitch, redbytes = (size_t)(KS - 1) * kW * RW * MT * 1024;
+    const int ntiles = (a.N + 15) / 16, groups = (ntiles + TW * RW - 1) / (TW * RW);
+    const size_t xbytes = (size_t)KS * 2 * 16 * MT * kXPitch, redbytes = (size_t)(KS - 1) * TW * RW * MT * 1024;
     const size_t shmem = std::max(xbytes, redbytes);
-    auto kern = gemm_mfma<MT, RW, D, KS>;
+    auto kern = gemm_mfma<MT, RW, D, KS, TW>;
     if (shmem > 65536) {                                     // above the default dynamic LDS limit (gfx950 has 160 KB)
       static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
       if (attr != hipSuccess) return attr;
     }
-    return launch(kern, dim3(groups, p.S), dim3(256 * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G,
-                  p.S, ctr, part, a.epi);
+    return launch(kern, dim3(groups, p.S), dim3(64 * TW * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K,
+                  a.G, p.S, ctr, part, a.epi);
+  }
+}
+
+// wider K-groups (5, 6 or 8 tile-waves) are built with one tile per wave and 2 ring slots only
+template <int MT>
+hipError_t dispatch_wide(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  const int ks = p.waves / p.KW;
+  switch (p.KW) {
+    case 5: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 5>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 5>(a, p, ctr, part);
+    case 6: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 6>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 6>(a, p, ctr, part);
+    default: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 8>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 8>(a, p, ctr, part);
   }
 }
 
@@ -486,6 +510,7 @@ hipError_t launch_tiles(const GemvArgs& a, int waves, int D) {
 
 template <int MT>
 hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
+  if (p.KW != kW) return dispatch_wide<MT>(a, p, ctr, part);
   switch (p.R) {
     case 1: return dispatch_ring<MT, 1>(a, p, ctr, part);
     default: return dispatch_ring<MT, 2>(a, p, ctr, part);
@@ -516,6 +541,29 @@ int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
 // 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP shapes at M = 48 and 64, while at M = 24..32
 // two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs 18.8 us at M = 24); a 3-slot ring for M <= 16
 // with up to two K-groups, else 2 slots.
+// tile-waves per K-group for one tile per wave: 4, or 5, 6 or 8 where that lets every workgroup run in one round on
+// the 256 CUs. A CU that receives a second workgroup of 4 tile-waves takes ~1.7x as long as one with a single
+// workgroup (3584 x 17408 at M = 64: 28.6 us with 272 workgroups, 3584 x 16384: 17.4 us with 256), so a layer of 1025
+// to 2048 tiles takes the fewest tile-waves that fit one round (MI355X graph sweep, M = 16..64: 3584 x 18944 with 237
+// workgroups of 5, M = 64 29.3 -> 23.0 us, M = 32 18.7 -> 14.1; 2048 x 22016 with 230 of 6, M = 64 18.7 -> 15.2;
+// 1536 x 17920 with 224 of 5, M = 64 15.0 -> 12.5). Past 2048 tiles, up to 48 rows, the count that leaves the fewest
+// tiles per CU, (workgroups / 256 rounded up) x tile-waves (3584 x 37888: 5, M = 32 27.9 -> 23.2 us); at 64 rows
+// those layers keep 4 (5 is 10% slower there).
+int balanced_tile_waves(int ntiles, int MT) {
+  constexpr int kCUs = 256;
+  if (ntiles <= kW * kCUs) return kW;
+  for (int tw : {5, 6, 8})
+    if ((ntiles + tw - 1) / tw <= kCUs) return tw;
+  if (MT > 3) return kW;
+  int best = kW;
+  long best_tiles = (long)((ntiles + kW - 1) / kW + kCUs - 1) / kCUs * kW;
+  for (int tw : {5, 6, 8}) {
+    const long tiles = (long)((ntiles + tw - 1) / tw + kCUs - 1) / kCUs * tw;
+    if (tiles < best_tiles) best = tw, best_tiles = tiles;
+  }
+  return best;
+}
+
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
   const GemvOverride o = gemv_override();
@@ -531,7 +579,9 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     return p;
   }
   p.R = row_tiles >= 2 ? 2 : 1;
-  const int groups = (ntiles + kW * p.R - 1) / (kW * p.R);
+  if (p.R == 1) p.KW = o.tile_waves > 0 ? o.tile_waves : balanced_tile_waves(ntiles, p.MT);
+  const int KW = p.KW;
+  const int groups = (ntiles + KW * p.R - 1) / (KW * p.R);
   const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
   int S = 1;
   if (o.splits > 0) {
@@ -545,19 +595,22 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   int ks = 1;
   if (o.waves >= 4) {
     ks = o.waves / 4;
+  } else if (KW != kW && groups <= 256) {                   // one round of wide K-groups: 2 K-groups at every M (the
+    ks = 2;                                                 // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us)
   } else if (p.MT <= 2) {
-    while (ks < 4 && (long)groups * S * kW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
+    while (ks < 4 && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
   } else {                                                  // from 33 rows: fewer, longer K-groups (see above)
-    while (ks < 4 && (long)groups * S * kW * 2 * ks <= kGemmMaxWavesWide && 2 * ks * S <= KC) ks *= 2;
+    while (ks < 4 && (long)groups * S * KW * 2 * ks <= kGemmMaxWavesWide && 2 * ks * S <= KC) ks *= 2;
   }
   while (ks > 1 && ks * S > KC) ks /= 2;
   p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);
-  while (!gemm_fits(p.MT, p.R, p.D, ks)) {                  // fewer K-groups, then fewer slots, then fewer tiles
+  if (KW != kW) p.D = 2;
+  while (!gemm_fits(p.MT, p.R, p.D, ks, KW)) {              // fewer K-groups, then fewer slots, then fewer tiles
     if (ks > 1) ks /= 2;
     else if (p.D > 2) --p.D;
     else p.R = 1;
   }
-  p.waves = kW * ks;
+  p.waves = KW * ks;
   p.S = std::max(S, 1);
   return p;
 }

@@ -50,6 +50,7 @@ struct GemvPlan {
   int S = 1;        // workgroups splitting K per row group (MFMA GEMM)
   int CS = 1;       // workgroups sharing a 16-row tile, 16 / CS rows each (MFMA-layout GEMV, R = 1)
   int TW = 0;       // MFMA GEMM: waves of the one-tile-per-workgroup kernel (0: the row-group kernel)
+  int KW = 4;       // MFMA GEMM row groups: tile-waves per K-group (4, or 5, 6, 8 with one tile per wave)
 };
 
 // launch shape of the prefill GEMM (M > 64)
@@ -70,6 +71,7 @@ struct GemvOverride {
   int ring = 0;
   int splits = 0;
   int gemm_kernel = 0;  // MFMA GEMM structure: 0 automatic, 1 row groups (K split across workgroups), 2 one tile each
+  int tile_waves = 0;   // MFMA GEMM row groups: tile-waves per K-group (0 automatic, 4, 5, 6 or 8)
 };
 GemvOverride gemv_override();
 
@@ -97,10 +99,12 @@ constexpr int kAttnMaxParts = 16;
 constexpr int kAttnManyBlocks = 512;      // from this many blocks on, at most 4 waves per block
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
-// (column tiles, row tiles per wave, ring slots, K-groups of 4 waves) the MFMA GEMM is built for: what fits the
-// register budget of 4 KS waves per workgroup without spilling (hipcc -O3, gfx950: 128 registers at 4 K-groups, 256 at
-// 2), and the LDS of the K-groups' x buffers
-constexpr bool gemm_fits(int MT, int RW, int D, int KS) {
+// (column tiles, row tiles per wave, ring slots, K-groups, tile-waves per K-group) the MFMA GEMM is built for: what
+// fits the register budget of TW KS waves per workgroup without spilling (hipcc -O3, gfx950: 128 registers at 16
+// waves, 168 at 9-12, 256 at up to 8), and the LDS of the K-groups' x buffers. K-groups of 5, 6 or 8 tile-waves are
+// built with one tile per wave, 2 slots and at most 2 K-groups.
+constexpr bool gemm_fits(int MT, int RW, int D, int KS, int TW = 4) {
+  if (TW != 4) return RW == 1 && D == 2 && KS <= 2 && (TW * KS <= 12 || MT <= 3);
   if (KS == 4) return D == 2 ? (RW == 1 ? MT <= 3 : MT <= 2) : (RW == 1 && MT == 1);
   if (KS == 2) return !((RW == 2 && (MT >= 3 ? D >= 3 : (MT == 2 && D == 4))) || (MT == 4 && RW == 1 && D == 4));
   return true;

@@ -18,7 +18,9 @@ from test_gpu_prefill import assert_rounds
 pytestmark = pytest.mark.gpu
 
 # (column tiles, row tiles per wave, ring slots, K-groups) the library builds: kernels.hpp gemm_fits
-def fits(mt, rw, d, ks):
+def fits(mt, rw, d, ks, tw=4):
+    if tw != 4:
+        return rw == 1 and d == 2 and ks <= 2 and (tw * ks <= 12 or mt <= 3)
     if ks == 4:
         return (mt <= 3 if rw == 1 else mt <= 2) if d == 2 else (rw == 1 and mt == 1)
     if ks == 2:
@@ -26,11 +28,12 @@ def fits(mt, rw, d, ks):
     return True
 
 
-def gemm(x, wq, rw, d, splits, ws, ks=0):
+def gemm(x, wq, rw, d, splits, ws, ks=0, tw=0):
     lib = _native.lib()
     n = wq.packed_mma.shape[0]
     y = torch.empty(x.shape[0], n, dtype=torch.half, device="cuda")
     _native.check(lib.lowbit_set_launch_override(4 * ks, d, splits))
+    _native.check(lib.lowbit_set_gemm_tile_waves(tw))
     try:
         _native.check(lib.lowbit_w4_gemm_mfma(_native.ptr(x), _native.ptr(wq.packed_mma), _native.ptr(wq.scales),
                                               _native.ptr(y), x.shape[0], n, x.shape[1], wq.group, rw,
@@ -39,6 +42,7 @@ def gemm(x, wq, rw, d, splits, ws, ks=0):
                                               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     finally:
         _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+        _native.check(lib.lowbit_set_gemm_tile_waves(0))
     return y
 
 
@@ -66,6 +70,44 @@ def test_every_launch_shape_against_fp64(cuda, k, n):
         assert rel(y0, ref) <= lim
     torch.cuda.synchronize()
     assert int(torch.count_nonzero(ws[:_native.WORKSPACE_COUNTER_BYTES])) == 0
+
+
+@pytest.mark.parametrize("k,n", [(1024, 16 * 37 + 5), (3584, 4096), (2048, 16 * 101)])
+def test_wider_k_groups_give_the_bits_of_four_tile_waves(cuda, k, n):
+    """K-groups of 5, 6 or 8 tile-waves (one tile per wave) compute every tile as K-groups of 4 do: the same chunks
+    per K-group in the same order, so the bits are the same, with and without a K split. The tile counts leave a
+    partial last workgroup, and 16 M rows over 5 or 6 waves a partial last round of x staging."""
+    wq, ref_w, *_, gen = make_weight(k, n, k + n, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for m in (1, 16, 17, 40, 64):
+        x = torch.randn(m, k, generator=gen).half().cuda()
+        ref = x.double() @ ref_w.T
+        lim = bound(x, ref_w, ref)
+        mt = (m + 15) // 16
+        for ks in (1, 2):
+            for splits in (1, 3):
+                base = gemm(x, wq, 1, 2, splits, ws, ks, tw=4)
+                assert rel(base, ref) <= lim, (k, n, m, ks, splits)
+                for tw in (5, 6, 8):
+                    if not fits(mt, 1, 2, ks, tw):
+                        continue
+                    y = gemm(x, wq, 1, 2, splits, ws, ks, tw)
+                    assert torch.equal(y, base), (k, n, m, ks, splits, tw)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(ws[:_native.WORKSPACE_COUNTER_BYTES])) == 0
+
+
+def test_automatic_tile_waves_balance_the_rounds(cuda):
+    """Past 1024 tiles the planner takes the fewest tile-waves that fit one round of workgroups (3584 x 18944: 1184
+    tiles -> 237 workgroups of 5, with 2 K-groups); the result equals that launch forced, bit for bit."""
+    wq, ref_w, *_, gen = make_weight(3584, 18944, 7, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for m in (24, 64):
+        x = torch.randn(m, 3584, generator=gen).half().cuda()
+        auto = ops.ext().w4_gemm_tc(x, wq.packed_mma, wq.scales, wq.group)
+        ref = x.double() @ ref_w.T
+        assert rel(auto, ref) <= bound(x, ref_w, ref)
+        assert torch.equal(auto, gemm(x, wq, 1, 2, 1, ws, 2, tw=5)), m
 
 
 def test_zero_weights_stay_zero_under_every_split(cuda):
