@@ -531,16 +531,6 @@ bool tiles_win(int MT, int ntiles, int KC) { return MT <= 4 && ntiles <= 288 && 
 // MT = 1 / 2 / 3 with 4 / 4 / 3 slots; MT = 4 spills at 3 slots)
 int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
 
-// Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
-// tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
-// N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
-// its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
-// split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
-// about kGemmTargetWaves waves run (M <= 32; from 33 rows K-groups double only while the waves stay within
-// kGemmMaxWavesWide: 3B gate/up at M = 64 12.3 us with 2 K-groups against 13.5 with 4, 7B gate/up 28.4 with 1 against
-// 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP shapes at M = 48 and 64, while at M = 24..32
-// two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs 18.8 us at M = 24); a 3-slot ring for M <= 16
-// with up to two K-groups, else 2 slots.
 // tile-waves per K-group for one tile per wave: 4, or 5, 6 or 8 where that lets every workgroup run in one round on
 // the 256 CUs. A CU that receives a second workgroup of 4 tile-waves takes ~1.7x as long as one with a single
 // workgroup (3584 x 17408 at M = 64: 28.6 us with 272 workgroups, 3584 x 16384: 17.4 us with 256), so a layer of 1025
@@ -564,6 +554,16 @@ int balanced_tile_waves(int ntiles, int MT) {
   return best;
 }
 
+// Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
+// tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
+// N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
+// its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
+// split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
+// about kGemmTargetWaves waves run (M <= 32, at most 4 up to 16 rows and 2 up to 32; from 33 rows K-groups double
+// only while the waves stay within kGemmMaxWavesWide: 3B gate/up at M = 64 12.3 us with 2 K-groups against 13.5 with
+// 4, 7B gate/up 28.4 with 1 against 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP shapes at
+// M = 48 and 64, while at M = 24..32 two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs 18.8 us at
+// M = 24); a 3-slot ring for M <= 16 with up to two K-groups of 4 tile-waves, else 2 slots.
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
   const GemvOverride o = gemv_override();
@@ -597,8 +597,9 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     ks = o.waves / 4;
   } else if (KW != kW && groups <= 256) {                   // one round of wide K-groups: 2 K-groups at every M (the
     ks = 2;                                                 // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us)
-  } else if (p.MT <= 2) {
-    while (ks < 4 && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
+  } else if (p.MT <= 2) {                                  // up to 4 K-groups for 16 rows, 2 for 32 (same sweep:
+    const int kmax = p.MT == 1 ? 4 : 2;                     // 2048 x 11008 at M = 32, 8.6 -> 8.2 us with 2)
+    while (ks < kmax && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
   } else {                                                  // from 33 rows: fewer, longer K-groups (see above)
     while (ks < 4 && (long)groups * S * KW * 2 * ks <= kGemmMaxWavesWide && 2 * ks * S <= KC) ks *= 2;
   }
