@@ -292,12 +292,24 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   for (int d = 0; d < D; ++d)                                // the last group, up to D wave-loads, without refills
     if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
 
-  // RoPE epilogue (M = 1): rows n (dim d of a head) and n + 8 (dim d + 64) -> bias, RoPE, q_out or the caches
-  auto rope_store = [&](int n, float v1, float v2) {
+  // RoPE epilogue (M = 1): rows n (dim d of a head) and n + 8 (dim d + 64) -> bias, RoPE, q_out or the caches. The
+  // position, the pair's two bias values and inv_freq[d] are requested together by rope_load (before the cross-wave
+  // reduction where there is one), so their round trip overlaps the reduction and is paid once, not twice (the
+  // position, then what the position check guarded)
+  struct RopeIn {
+    int64_t p;
+    f16 b1, b2;
+    float invf;
+  };
+  auto rope_load = [&](int n) -> RopeIn {
+    const int pj = n & 127, d = 8 * (pj >> 4) + (pj & 7);
+    return RopeIn{epi.rope.pos[0], epi.aux[n], epi.aux[n + 8], epi.rope.inv_freq[d]};
+  };
+  auto rope_store = [&](int n, float v1, float v2, const RopeIn& in) {
     const RopeArgs& ra = epi.rope;
-    const int64_t p = ra.pos[0];
+    const int64_t p = in.p;
     if (p < 0 || p >= ra.L) return;                         // the host checks positions; never write out of bounds
-    const f16 x1 = (f16)v1 + epi.aux[n], x2 = (f16)v2 + epi.aux[n + 8];
+    const f16 x1 = (f16)v1 + in.b1, x2 = (f16)v2 + in.b2;
     const int hh = n >> 7, pj = n & 127, d = 8 * (pj >> 4) + (pj & 7);
     if (hh >= ra.Hq + ra.Hkv) {
       f16* dst = ra.v_cache + ((size_t)(hh - ra.Hq - ra.Hkv) * ra.L + p) * 128;
@@ -306,7 +318,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       return;
     }
     f16 o1, o2;
-    rope_pair(x1, x2, p, ra.inv_freq[d], o1, o2);
+    rope_pair(x1, x2, p, in.invf, o1, o2);
     f16* dst = hh < ra.Hq ? ra.q_out + (size_t)hh * 128 : ra.k_cache + ((size_t)(hh - ra.Hq) * ra.L + p) * 128;
     dst[d] = o1;
     dst[d + 64] = o2;
@@ -333,13 +345,20 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
           const float up = shfl_down32(v);
           if (q == 0 && r < 8 && n < N) {
             if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + r] = silu_mul(v, up);
-            else rope_store(n, v, up);
+            else rope_store(n, v, up, rope_load(n));
           }
         } else if (q == 0 && cs == 0 && n < N) {
           y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
         }
       }
     return;
+  }
+  // the RoPE inputs of the first pair this thread stores below, requested before the reduction's barriers
+  RopeIn rope_first{};
+  {
+    const int idx = threadIdx.x, i = idx / (M * RS), rr = idx % RS;
+    const int n = 16 * (t0 + i) + RS * sub + rr;
+    if (pairs && epi.mode == kEpiRopeQKV && idx < R * M * RS && rr < 8 && n < N) rope_first = rope_load(n);
   }
   float* red = reinterpret_cast<float*>(smem);              // x is dead after the barrier below
   __syncthreads();
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
         u += red[wv2 * (R * M * RS) + idx + 8];
       }
       if (epi.mode == kEpiSiluMul) y[(size_t)m * (N / 2) + 8 * (t0 + i) + rr] = silu_mul(g, u);
-      else rope_store(n, g, u);
+      else rope_store(n, g, u, idx == (int)threadIdx.x ? rope_first : rope_load(n));
       continue;
     }
     float v = 0.f;
