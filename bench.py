@@ -89,7 +89,7 @@ def parse():
     ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles", "tilewaves"], default=None,
                     help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
                          "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32; "
-                         "tilewaves: the row groups' tile-waves per K-group on layers past 1024 tiles")
+                         "tilewaves: the row groups' tile-waves and K-groups on layers of 560 to 2368 tiles")
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
@@ -638,15 +638,24 @@ def sweep_tiles(a):
 
 
 def sweep_tilewaves(a):
-    """MFMA GEMM (v5) row groups on the layers past 1024 tiles (and two at or below it), M in {16, 32, 48, 64}:
-    graph-timed us per call of the automatic plan, of 4 tile-waves per K-group (lowbit_set_gemm_tile_waves(4), the
-    rest automatic) and of 5, 6 and 8 tile-waves with 1 or 2 K-groups."""
+    """MFMA GEMM (v5) row groups on layers of 560 to 2368 tiles, M in {16, 32, 48, 64}: graph-timed us per call of the
+    automatic plan, of 4 tile-waves per K-group (lowbit_set_gemm_tile_waves(4), the rest automatic) and of 3, 4, 5, 6
+    and 8 tile-waves with 1, 2 or 4 K-groups, where the library builds them."""
     import torch
     from lowbit import _native, ops
     torch.cuda.set_device(0)
     lib = _native.lib()
+
+    def built(tw, ks, mt):                                 # kernels.hpp gemm_fits with one tile per wave, 2 slots
+        if tw == 3:
+            return ks <= 2 or mt <= 2
+        if tw == 4:
+            return ks <= 2 or mt <= 3
+        return ks <= 2 and (tw * ks <= 12 or mt <= 3)
+
     rows = []
-    for k, n in ((3584, 18944), (2048, 22016), (1536, 17920), (3584, 37888), (2048, 11008), (3584, 16384)):
+    for k, n in ((3584, 18944), (2048, 22016), (1536, 17920), (3584, 37888), (2048, 11008), (1536, 8960),
+                 (3584, 16384)):
         cl = cloned_copies(torch, ops, k, n)
         for m in (16, 32, 48, 64):
             x = torch.randn(m, k, device="cuda").half()
@@ -655,12 +664,12 @@ def sweep_tilewaves(a):
             try:
                 _native.check(lib.lowbit_set_gemm_tile_waves(4))
                 r["tw4"] = t()
-                for tw in (5, 6, 8):
-                    for ks in (1, 2):
-                        if tw * ks > 12 and m > 48:            # never built (register budget)
+                for tw in (3, 4, 5, 6, 8):
+                    for ks in (1, 2, 4):
+                        if not built(tw, ks, (m + 15) // 16):
                             continue
                         _native.check(lib.lowbit_set_gemm_tile_waves(tw))
-                        _native.check(lib.lowbit_set_launch_override(4 * ks, 0, 0))
+                        _native.check(lib.lowbit_set_launch_override(4 * ks, 2, 0))
                         r[f"tw{tw}_kg{ks}"] = t()
                         _native.check(lib.lowbit_set_launch_override(0, 0, 0))
             finally:

@@ -74,8 +74,8 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 int lowbit_set_gemm_kernel(int kernel);
 
 /* Process-wide choice of the MFMA GEMM's tile-waves per K-group in its row-group structure, for tuning sweeps and
- * tests: 0 = automatic; 4, 5, 6 or 8 (5, 6 and 8 with one 16-row tile per wave, 2 ring slots and at most 2 K-groups;
- * with row_tiles = 2 the GEMM keeps 4). Each tile is computed the same way whatever the count, so the results are
+ * tests: 0 = automatic; 3, 4, 5, 6 or 8 (all but 4 with one 16-row tile per wave and 2 ring slots; 3 with up to 4
+ * K-groups at M <= 32, else 2, 5, 6 and 8 with at most 2; with row_tiles = 2 the GEMM keeps 4). Each tile is computed the same way whatever the count, so the results are
  * identical bit for bit. Affects later launches only. No counterpart in the reference. */
 int lowbit_set_gemm_tile_waves(int tile_waves);
 

@@ -204,8 +204,8 @@ int lowbit_set_gemm_kernel(int kernel) {
 }
 
 int lowbit_set_gemm_tile_waves(int tile_waves) {
-  if (!(tile_waves == 0 || tile_waves == 4 || tile_waves == 5 || tile_waves == 6 || tile_waves == 8))
-    return fail(LOWBIT_ERR_TUNING, "tile_waves is 0 (auto), 4, 5, 6 or 8");
+  if (!(tile_waves == 0 || tile_waves == 3 || tile_waves == 4 || tile_waves == 5 || tile_waves == 6 || tile_waves == 8))
+    return fail(LOWBIT_ERR_TUNING, "tile_waves is 0 (auto), 3, 4, 5, 6 or 8");
   g_override_tile_waves.store(tile_waves, std::memory_order_relaxed);
   return ok();
 }

@@ -458,11 +458,14 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
   }
 }
 
-// wider K-groups (5, 6 or 8 tile-waves) are built with one tile per wave and 2 ring slots only
+// K-groups of 3, 5, 6 or 8 tile-waves are built with one tile per wave and 2 ring slots only
 template <int MT>
 hipError_t dispatch_wide(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
   const int ks = p.waves / p.KW;
   switch (p.KW) {
+    case 3:
+      return ks == 1 ? launch_gemm<MT, 1, 2, 1, 3>(a, p, ctr, part)
+           : ks == 2 ? launch_gemm<MT, 1, 2, 2, 3>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 4, 3>(a, p, ctr, part);
     case 5: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 5>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 5>(a, p, ctr, part);
     case 6: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 6>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 6>(a, p, ctr, part);
     default: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 8>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 8>(a, p, ctr, part);
@@ -532,15 +535,18 @@ bool tiles_win(int MT, int ntiles, int KC) { return MT <= 4 && ntiles <= 288 && 
 int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
 
 // tile-waves per K-group for one tile per wave: 4, or 5, 6 or 8 where that lets every workgroup run in one round on
-// the 256 CUs. A CU that receives a second workgroup of 4 tile-waves takes ~1.7x as long as one with a single
-// workgroup (3584 x 17408 at M = 64: 28.6 us with 272 workgroups, 3584 x 16384: 17.4 us with 256), so a layer of 1025
-// to 2048 tiles takes the fewest tile-waves that fit one round (MI355X graph sweep, M = 16..64: 3584 x 18944 with 237
-// workgroups of 5, M = 64 29.3 -> 23.0 us, M = 32 18.7 -> 14.1; 2048 x 22016 with 230 of 6, M = 64 18.7 -> 15.2;
-// 1536 x 17920 with 224 of 5, M = 64 15.0 -> 12.5). Past 2048 tiles, up to 48 rows, the count that leaves the fewest
-// tiles per CU, (workgroups / 256 rounded up) x tile-waves (3584 x 37888: 5, M = 32 27.9 -> 23.2 us); at 64 rows
-// those layers keep 4 (5 is 10% slower there).
+// the 256 CUs, or 3 where 4 would leave CUs idle. A CU that receives a second workgroup of 4 tile-waves takes ~1.7x as
+// long as one with a single workgroup (3584 x 17408 at M = 64: 28.6 us with 272 workgroups, 3584 x 16384: 17.4 us
+// with 256), so a layer of 1025 to 2048 tiles takes the fewest tile-waves that fit one round (MI355X graph sweep,
+// M = 16..64: 3584 x 18944 with 237 workgroups of 5, M = 64 29.3 -> 23.0 us, M = 32 18.7 -> 14.1; 2048 x 22016 with
+// 230 of 6, M = 64 18.7 -> 15.2; 1536 x 17920 with 224 of 5, M = 64 15.0 -> 12.5). Past 2048 tiles, up to 48 rows, the
+// count that leaves the fewest tiles per CU, (workgroups / 256 rounded up) x tile-waves (3584 x 37888: 5, M = 32
+// 27.9 -> 23.2 us); at 64 rows those layers keep 4 (5 is 10% slower there). A layer of 385 to 768 tiles takes 3, so
+// that its 129-256 workgroups occupy more CUs than the 97-192 of 4 (2048 x 11008: M = 16 6.90 -> 6.51 us, M = 48
+// 9.84 -> 9.57; 1536 x 8960: M = 16 6.09 -> 5.81; 2048 x 8192 at M = 48 10.5 -> 9.3; level at M = 32 and 64).
 int balanced_tile_waves(int ntiles, int MT) {
   constexpr int kCUs = 256;
+  if (ntiles > 3 * 128 && ntiles <= 3 * kCUs) return 3;
   if (ntiles <= kW * kCUs) return kW;
   for (int tw : {5, 6, 8})
     if ((ntiles + tw - 1) / tw <= kCUs) return tw;
@@ -559,11 +565,12 @@ int balanced_tile_waves(int ntiles, int MT) {
 // N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
 // its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
 // split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
-// about kGemmTargetWaves waves run (M <= 32, at most 4 up to 16 rows and 2 up to 32; from 33 rows K-groups double
-// only while the waves stay within kGemmMaxWavesWide: 3B gate/up at M = 64 12.3 us with 2 K-groups against 13.5 with
-// 4, 7B gate/up 28.4 with 1 against 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP shapes at
-// M = 48 and 64, while at M = 24..32 two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs 18.8 us at
-// M = 24); a 3-slot ring for M <= 16 with up to two K-groups of 4 tile-waves, else 2 slots.
+// about kGemmTargetWaves waves run (at most 2 K-groups for 17..32 rows; up to 16 rows 4, also where the row groups
+// alone reach that many waves: 3584 x 16384, 256 row groups, M = 16, 10.3 -> 9.6 us against 2); from 33 rows K-groups
+// double only while the waves stay within kGemmMaxWavesWide (3B gate/up at M = 64 12.3 us with 2 K-groups against
+// 13.5 with 4, 7B gate/up 28.4 with 1 against 29.1 with 2, best or within 1% of best on the eight 1.5B / 3B / 7B MLP
+// shapes at M = 48 and 64, while at M = 24..32 two K-groups stay faster on the widest layers: 7B gate/up 17.9 vs
+// 18.8 us at M = 24); a 3-slot ring for M <= 16 with up to two K-groups of 4 tile-waves, else 2 slots.
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes) {
   GemvPlan p;
   const GemvOverride o = gemv_override();
@@ -595,8 +602,10 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   int ks = 1;
   if (o.waves >= 4) {
     ks = o.waves / 4;
-  } else if (KW != kW && groups <= 256) {                   // one round of wide K-groups: 2 K-groups at every M (the
-    ks = 2;                                                 // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us)
+  } else if (KW != kW && groups <= 256) {                   // one round of 3, 5, 6 or 8 tile-waves: 2 K-groups (the
+    ks = KW == 3 && p.MT == 1 ? 4 : 2;                      // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us), 4
+  } else if (p.MT == 1 && S == 1) {                         // for 3 tile-waves at 16 rows (2048 x 11008: 7.22 -> 6.51)
+    while (ks < 4 && 2 * ks <= KC) ks *= 2;
   } else if (p.MT <= 2) {                                  // up to 4 K-groups for 16 rows, 2 for 32 (same sweep:
     const int kmax = p.MT == 1 ? 4 : 2;                     // 2048 x 11008 at M = 32, 8.6 -> 8.2 us with 2)
     while (ks < kmax && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;

@@ -71,7 +71,7 @@ struct GemvOverride {
   int ring = 0;
   int splits = 0;
   int gemm_kernel = 0;  // MFMA GEMM structure: 0 automatic, 1 row groups (K split across workgroups), 2 one tile each
-  int tile_waves = 0;   // MFMA GEMM row groups: tile-waves per K-group (0 automatic, 4, 5, 6 or 8)
+  int tile_waves = 0;   // MFMA GEMM row groups: tile-waves per K-group (0 automatic, 3, 4, 5, 6 or 8)
 };
 GemvOverride gemv_override();
 
@@ -101,9 +101,10 @@ constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;
 // (column tiles, row tiles per wave, ring slots, K-groups, tile-waves per K-group) the MFMA GEMM is built for: what
 // fits the register budget of TW KS waves per workgroup without spilling (hipcc -O3, gfx950: 128 registers at 16
-// waves, 168 at 9-12, 256 at up to 8), and the LDS of the K-groups' x buffers. K-groups of 5, 6 or 8 tile-waves are
-// built with one tile per wave, 2 slots and at most 2 K-groups.
+// waves, 168 at 9-12, 256 at up to 8), and the LDS of the K-groups' x buffers. K-groups of 3, 5, 6 or 8 tile-waves
+// are built with one tile per wave and 2 slots, at most 2 K-groups (4 of 3 tile-waves up to 32 rows).
 constexpr bool gemm_fits(int MT, int RW, int D, int KS, int TW = 4) {
+  if (TW == 3) return RW == 1 && D == 2 && (KS <= 2 || MT <= 2);
   if (TW != 4) return RW == 1 && D == 2 && KS <= 2 && (TW * KS <= 12 || MT <= 3);
   if (KS == 4) return D == 2 ? (RW == 1 ? MT <= 3 : MT <= 2) : (RW == 1 && MT == 1);
   if (KS == 2) return !((RW == 2 && (MT >= 3 ? D >= 3 : (MT == 2 && D == 4))) || (MT == 4 && RW == 1 && D == 4));

@@ -68,7 +68,7 @@ def _msg(rc):
     (lambda l: l.lowbit_set_launch_override(4, 4, 33), 8, "k_splits"),
     (lambda l: l.lowbit_set_gemm_kernel(3), 8, "kernel is 0"),
     (lambda l: l.lowbit_set_gemm_kernel(-1), 8, "kernel is 0"),
-    (lambda l: l.lowbit_set_gemm_tile_waves(3), 8, "tile_waves is 0"),
+    (lambda l: l.lowbit_set_gemm_tile_waves(2), 8, "tile_waves is 0"),
     (lambda l: l.lowbit_set_gemm_tile_waves(7), 8, "tile_waves is 0"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 5, 16, 128, None), 5, "1..4 rows"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 1, 16, 12, None), 3, "K % 8"),

@@ -19,6 +19,8 @@ pytestmark = pytest.mark.gpu
 
 # (column tiles, row tiles per wave, ring slots, K-groups) the library builds: kernels.hpp gemm_fits
 def fits(mt, rw, d, ks, tw=4):
+    if tw == 3:
+        return rw == 1 and d == 2 and (ks <= 2 or mt <= 2)
     if tw != 4:
         return rw == 1 and d == 2 and ks <= 2 and (tw * ks <= 12 or mt <= 3)
     if ks == 4:
@@ -73,10 +75,10 @@ def test_every_launch_shape_against_fp64(cuda, k, n):
 
 
 @pytest.mark.parametrize("k,n", [(1024, 16 * 37 + 5), (3584, 4096), (2048, 16 * 101)])
-def test_wider_k_groups_give_the_bits_of_four_tile_waves(cuda, k, n):
-    """K-groups of 5, 6 or 8 tile-waves (one tile per wave) compute every tile as K-groups of 4 do: the same chunks
+def test_k_group_widths_give_the_bits_of_four_tile_waves(cuda, k, n):
+    """K-groups of 3, 5, 6 or 8 tile-waves (one tile per wave) compute every tile as K-groups of 4 do: the same chunks
     per K-group in the same order, so the bits are the same, with and without a K split. The tile counts leave a
-    partial last workgroup, and 16 M rows over 5 or 6 waves a partial last round of x staging."""
+    partial last workgroup, and 16 M rows over 3, 5 or 6 waves a partial last round of x staging."""
     wq, ref_w, *_, gen = make_weight(k, n, k + n, layouts=("mma",))
     ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     for m in (1, 16, 17, 40, 64):
@@ -84,11 +86,13 @@ def test_wider_k_groups_give_the_bits_of_four_tile_waves(cuda, k, n):
         ref = x.double() @ ref_w.T
         lim = bound(x, ref_w, ref)
         mt = (m + 15) // 16
-        for ks in (1, 2):
+        for ks in (1, 2, 4):
+            if not fits(mt, 1, 2, ks):
+                continue
             for splits in (1, 3):
                 base = gemm(x, wq, 1, 2, splits, ws, ks, tw=4)
                 assert rel(base, ref) <= lim, (k, n, m, ks, splits)
-                for tw in (5, 6, 8):
+                for tw in (3, 5, 6, 8):
                     if not fits(mt, 1, 2, ks, tw):
                         continue
                     y = gemm(x, wq, 1, 2, splits, ws, ks, tw)
@@ -108,6 +112,21 @@ def test_automatic_tile_waves_balance_the_rounds(cuda):
         ref = x.double() @ ref_w.T
         assert rel(auto, ref) <= bound(x, ref_w, ref)
         assert torch.equal(auto, gemm(x, wq, 1, 2, 1, ws, 2, tw=5)), m
+
+
+@pytest.mark.parametrize("n,cases", [(16 * 700, ((8, 3, 4), (40, 3, 2))), (16 * 1000, ((16, 4, 4),))])
+def test_automatic_k_groups_fill_the_cus(cuda, n, cases):
+    """Layers of 385-768 tiles take K-groups of 3 tile-waves (700 tiles -> 234 workgroups), 4 of them up to 16 rows
+    and 2 beyond; up to 16 rows a layer of 256 row groups still takes 4 K-groups. Each result equals that launch
+    forced, bit for bit."""
+    wq, ref_w, *_, gen = make_weight(1024, n, 11, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    for m, tw, ks in cases:
+        x = torch.randn(m, 1024, generator=gen).half().cuda()
+        auto = ops.ext().w4_gemm_tc(x, wq.packed_mma, wq.scales, wq.group)
+        ref = x.double() @ ref_w.T
+        assert rel(auto, ref) <= bound(x, ref_w, ref)
+        assert torch.equal(auto, gemm(x, wq, 1, 2, 1, ws, ks, tw=tw)), (n, m)
 
 
 def test_zero_weights_stay_zero_under_every_split(cuda):
