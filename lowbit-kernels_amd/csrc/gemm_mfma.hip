@@ -37,7 +37,15 @@ namespace lowbit {
 namespace {
 
 constexpr int kW = 4;              // tile-waves per K-group of the default shape
-constexpr int kXPitch = 272;       // bytes per staged activation row (256 + 16: conflict-free 16-byte LDS reads)
+constexpr int kXPitch = 256;       // bytes per staged activation row (one 128-k chunk of fp16)
+// 16-byte block b of staged x row m sits at block b ^ xswz(m % 16) of the row. A lane (r = m % 16, q) reading k-step j
+// of a B fragment takes block b = 4 q + j, which lands at 4 (q ^ (r & 3)) + (j ^ (r >> 2)): each wave-wide fragment
+// read covers all 16 block positions of 16 rows. An MI355X probe of those reads (16 ds_read_b128 per wave with
+// immediate offsets, 10 and 16 waves per CU): 168 / 209 B/clk per CU, against 105 / 113 for rows padded to 272 bytes
+// (the layout before), 108 / 117 for b ^ r and 116 / 123 for 288-byte rows; the staging stores run at 73 B/clk in all
+// of these layouts. In the kernel: 7B gate/up at M = 64 22.8 -> 21.0 us, 7B down 32.3 -> 31.5, 3B merged gate|up
+// 15.4 -> 14.8 (a few shapes at 48 rows lose up to 3%: 2048 x 11008 9.5 -> 9.85).
+constexpr int xswz(int r) { return ((r & 3) << 2) | (r >> 2); }
 }  // namespace
 
 template <int MT, int RW, int D, int KS, int TW>
@@ -91,7 +99,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
     const int pc = gt + kGroupThreads * u;
     const bool in = kWhole || pc < kPieces;
     xoff[u] = in ? ((pc >> 4) * K + 8 * (pc & 15)) * 2 : kOutOfRange;
-    xl[u] = in ? (pc >> 4) * kXPitch + 16 * (pc & 15) : -1;
+    xl[u] = in ? (pc >> 4) * kXPitch + 16 * ((pc & 15) ^ xswz((pc >> 4) & 15)) : -1;
   }
   auto piece_live = [&](int u) { return kWhole || u + 1 < kPer || xl[u] >= 0; };
 
@@ -127,6 +135,9 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const DecodeRegs dc = decode_regs();
+  int xrd[4];                                               // lane (r, q): block 4 q + j of row r, swizzled
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xrd[j] = r * kXPitch + 16 * ((4 * q + j) ^ xswz(r));
 
   auto consume = [&](int d, int b) {
     f32x4 pt[RW][MT];
@@ -139,7 +150,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
       f16x8 bx[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        bx[mt] = *reinterpret_cast<const f16x8*>(xbuf + b * kXBuf + (16 * mt + r) * kXPitch + 16 * (4 * q + j));
+        bx[mt] = *reinterpret_cast<const f16x8*>(xbuf + b * kXBuf + 16 * mt * kXPitch + xrd[j]);
 #pragma unroll
       for (int i = 0; i < RW; ++i) {
         const f16x8 a = decode_word_a(rw[d][i][j], dc);
@@ -541,12 +552,12 @@ int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
 // M = 16..64: 3584 x 18944 with 237 workgroups of 5, M = 64 29.3 -> 23.0 us, M = 32 18.7 -> 14.1; 2048 x 22016 with
 // 230 of 6, M = 64 18.7 -> 15.2; 1536 x 17920 with 224 of 5, M = 64 15.0 -> 12.5). Past 2048 tiles, up to 48 rows, the
 // count that leaves the fewest tiles per CU, (workgroups / 256 rounded up) x tile-waves (3584 x 37888: 5, M = 32
-// 27.9 -> 23.2 us); at 64 rows those layers keep 4 (5 is 10% slower there). A layer of 385 to 768 tiles takes 3, so
-// that its 129-256 workgroups occupy more CUs than the 97-192 of 4 (2048 x 11008: M = 16 6.90 -> 6.51 us, M = 48
-// 9.84 -> 9.57; 1536 x 8960: M = 16 6.09 -> 5.81; 2048 x 8192 at M = 48 10.5 -> 9.3; level at M = 32 and 64).
+// 27.9 -> 23.2 us); at 64 rows those layers keep 4 (5 is 10% slower there). Up to 16 rows a layer of 385 to 768
+// tiles takes 3, so that its 129-256 workgroups occupy more CUs than the 97-192 of 4 (2048 x 11008: 6.82 -> 6.46 us;
+// 1536 x 8960: 6.04 -> 5.78); from 17 rows 4 is level or up to 3% faster.
 int balanced_tile_waves(int ntiles, int MT) {
   constexpr int kCUs = 256;
-  if (ntiles > 3 * 128 && ntiles <= 3 * kCUs) return 3;
+  if (MT == 1 && ntiles > 3 * 128 && ntiles <= 3 * kCUs) return 3;
   if (ntiles <= kW * kCUs) return kW;
   for (int tw : {5, 6, 8})
     if ((ntiles + tw - 1) / tw <= kCUs) return tw;
@@ -604,7 +615,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     ks = o.waves / 4;
   } else if (KW != kW && groups <= 256) {                   // one round of 3, 5, 6 or 8 tile-waves: 2 K-groups (the
     ks = KW == 3 && p.MT == 1 ? 4 : 2;                      // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us), 4
-  } else if (p.MT == 1 && S == 1) {                         // for 3 tile-waves at 16 rows (2048 x 11008: 7.22 -> 6.51)
+  } else if (p.MT == 1 && S == 1) {                         // for 3 tile-waves at 16 rows (2048 x 11008: 7.19 -> 6.46)
     while (ks < 4 && 2 * ks <= KC) ks *= 2;
   } else if (p.MT <= 2) {                                  // up to 4 K-groups for 16 rows, 2 for 32 (same sweep:
     const int kmax = p.MT == 1 ? 4 : 2;                     // 2048 x 11008 at M = 32, 8.6 -> 8.2 us with 2)

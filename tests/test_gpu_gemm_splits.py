@@ -114,11 +114,11 @@ def test_automatic_tile_waves_balance_the_rounds(cuda):
         assert torch.equal(auto, gemm(x, wq, 1, 2, 1, ws, 2, tw=5)), m
 
 
-@pytest.mark.parametrize("n,cases", [(16 * 700, ((8, 3, 4), (40, 3, 2))), (16 * 1000, ((16, 4, 4),))])
+@pytest.mark.parametrize("n,cases", [(16 * 700, ((8, 3, 4), (40, 4, 2))), (16 * 1000, ((16, 4, 4),))])
 def test_automatic_k_groups_fill_the_cus(cuda, n, cases):
-    """Layers of 385-768 tiles take K-groups of 3 tile-waves (700 tiles -> 234 workgroups), 4 of them up to 16 rows
-    and 2 beyond; up to 16 rows a layer of 256 row groups still takes 4 K-groups. Each result equals that launch
-    forced, bit for bit."""
+    """Up to 16 rows, layers of 385-768 tiles take 4 K-groups of 3 tile-waves (700 tiles -> 234 workgroups) and a
+    layer of 256 row groups of 4 still takes 4 K-groups; beyond 16 rows the 700 tiles keep 4 tile-waves, 2 K-groups.
+    Each result equals that launch forced, bit for bit."""
     wq, ref_w, *_, gen = make_weight(1024, n, 11, layouts=("mma",))
     ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     for m, tw, ks in cases:
