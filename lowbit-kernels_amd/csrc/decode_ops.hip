@@ -251,6 +251,148 @@ __global__ __launch_bounds__(256) void attention_combine(const float* __restrict
   out[((size_t)m * Hq + h) * kHeadDim + d] = (f16)(num / den);
 }
 
+// Causal GQA attention on MFMA for multi-token steps and prompts (same contract as attention_kernel): one wave per
+// (KV head, 16 query rows, key partition), the query rows of a KV head numbered row = token * G + head-in-group.
+// Per block of 32 keys (v_mfma_f32_16x16x32_f16):
+//   S^T = K Q^T: A = 16 keys x 32 dims (lane (r, c): key kb + 8 (r / 4) + r % 4 + 4 t, 16 bytes of its row), B = the
+//   wave's 16 query rows x 32 dims (held in registers), two key tiles t x four 32-dim steps; the key order is chosen so
+//   that lane (r, c) ends up with the scores of query row r at keys kb + 8 c .. kb + 8 c + 7;
+//   online softmax per query row (max and sum over the four lanes r, r + 16, r + 32, r + 48), masked past the row's
+//   position; the probabilities, split into an fp16 head and an fp16 remainder (together exact to ~2^-22), are the
+//   B operands of the next product (two MFMAs per dim tile, so the weights carry fp32 accuracy as in
+//   attention_kernel);
+//   O^T += V^T P^T: A = 16 dims x 32 keys of V^T, which the wave writes to its own LDS from its 8 KB of V rows
+//   (4 keys x 8 dims per lane, packed into 8-byte rows of V^T) and reads back as 16-byte fragments; eight dim tiles.
+// A wave touches only its own LDS, in order, so no barrier is needed. With P > 1 each wave writes the partial (max,
+// sum, unnormalized output) of its rows in attention_kernel's layout and attention_combine merges them.
+constexpr int kAttnVtPitch = 80;                            // bytes per dim row of the staged V^T (64 + 16 padding)
+
+__global__ __launch_bounds__(64) void attention_mfma(const f16* __restrict__ q, const f16* __restrict__ k_cache,
+                                                     const f16* __restrict__ v_cache, const int64_t* __restrict__ pos,
+                                                     f16* __restrict__ out, int M, int Hq, int Hkv, int L, float scale,
+                                                     float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) uint8_t vt[kHeadDim * kAttnVtPitch];
+  args_in_sgprs(q, k_cache, v_cache, pos, out, M, Hq, Hkv, L, part);
+  const int G = Hq / Hkv, P = gridDim.y, pid = blockIdx.y;
+  const int hk = blockIdx.x % Hkv, tile = blockIdx.x / Hkv;
+  const int lane = threadIdx.x, r = lane & 15, c = lane >> 4;
+  // this lane's query row (as the B column r)
+  const int row = 16 * tile + r, m = row / G, g = row - m * G;
+  const bool live = m < M;
+  const int pr = live ? (int)min((int64_t)L - 1, pos[m]) : -1;  // last key the row attends
+  int wmax = pr;                                               // the wave's last key
+  wmax = max(wmax, __shfl_xor(wmax, 1, 64));
+  wmax = max(wmax, __shfl_xor(wmax, 2, 64));
+  wmax = max(wmax, __shfl_xor(wmax, 4, 64));
+  wmax = max(wmax, __shfl_xor(wmax, 8, 64));
+  // the P partitions split the keys this wave attends (not the caller's bound on them) in whole 32-key blocks
+  const int ch = ((wmax + 1 + P - 1) / P + 31) / 32 * 32;
+  const int kbeg = pid * ch, kend = min(wmax + 1, kbeg + ch);
+  const __amdgpu_buffer_rsrc_t qr = make_rsrc(q, (uint32_t)M * (uint32_t)Hq * kHeadDim * 2u);
+  const int qoff = live ? ((m * Hq + hk * G + g) * kHeadDim + 8 * c) * 2 : kOutOfRange;
+  f16x8 qf[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) qf[ks] = __builtin_bit_cast(f16x8, buffer_load16(qr, qoff + 64 * ks));
+  const f16* kh = k_cache + (size_t)hk * L * kHeadDim;
+  const f16* vh = v_cache + (size_t)hk * L * kHeadDim;
+  const int kr = 8 * (r >> 2) + (r & 3);                      // key of A row r in tile 0 (tile 1: + 4)
+  float mx = -INFINITY, lsum = 0.f;
+  f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int kb = kbeg; kb < kend; kb += 32) {
+    u32x4 kf[2][4], vf[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f16* krow = kh + (size_t)min(kb + kr + 4 * t, L - 1) * kHeadDim + 8 * c;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[t][ks] = *reinterpret_cast<const u32x4*>(krow + 32 * ks);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)                               // V rows kb + 4 (lane % 8) + j, dims 8 (lane / 8 + 8 u)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        vf[u][j] = *reinterpret_cast<const u32x4*>(vh + (size_t)min(kb + 4 * (lane & 7) + j, L - 1) * kHeadDim +
+                                                   8 * ((lane >> 3) + 8 * u));
+    f32x4 st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kf[t][ks]), qf[ks], st[t], 0, 0, 0);
+    }
+    // V^T rows (dim) x 4 keys per lane into the wave's LDS
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int d0 = 8 * ((lane >> 3) + 8 * u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {                           // dims d0 + 2 e, d0 + 2 e + 1
+        const uint32_t a0 = vf[u][0][e], a1 = vf[u][1][e], a2 = vf[u][2][e], a3 = vf[u][3][e];
+        // v_perm picks bytes of {a1, a0}: 0x05040100 the low halves (a0, a1), 0x07060302 the high halves
+        const uint2 lo = make_uint2(__builtin_amdgcn_perm(a1, a0, 0x05040100u),
+                                    __builtin_amdgcn_perm(a3, a2, 0x05040100u));
+        const uint2 hi = make_uint2(__builtin_amdgcn_perm(a1, a0, 0x07060302u),
+                                    __builtin_amdgcn_perm(a3, a2, 0x07060302u));
+        *reinterpret_cast<uint2*>(vt + (d0 + 2 * e) * kAttnVtPitch + 8 * (lane & 7)) = lo;
+        *reinterpret_cast<uint2*>(vt + (d0 + 2 * e + 1) * kAttnVtPitch + 8 * (lane & 7)) = hi;
+      }
+    }
+    // scores of row r at keys kb + 8 c + i (i = 4 t + v), masked past the row's position and the partition
+    float sc[8], bm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = kb + 8 * c + i;
+      sc[i] = key <= pr && key < kend ? st[i >> 2][i & 3] * scale : -INFINITY;
+      bm = fmaxf(bm, sc[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float nm = fmaxf(mx, bm);
+    const float corr = nm == -INFINITY ? 1.f : __expf(mx - nm);   // 0 on the first block with a key
+    f16x8 ph, pl;                                           // p = ph + pl to ~2^-22: fp32-accurate weights
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float pj = nm == -INFINITY ? 0.f : __expf(sc[i] - nm);
+      ps += pj;
+      ph[i] = (f16)pj;
+      pl[i] = (f16)(pj - (float)ph[i]);
+    }
+    lsum = lsum * corr + ps;
+    mx = nm;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f16x8 va = *reinterpret_cast<const f16x8*>(vt + (16 * dt + r) * kAttnVtPitch + 16 * c);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt] * corr, 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
+    }
+  }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  if (!live) return;
+  // lane (r, c) holds O^T[16 dt + 4 c + v][row r]
+  if (P == 1) {
+    f16* dst = out + ((size_t)m * Hq + hk * G + g) * kHeadDim + 4 * c;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f16x2 lo = {(f16)(o[dt][0] / lsum), (f16)(o[dt][1] / lsum)};
+      const f16x2 hi = {(f16)(o[dt][2] / lsum), (f16)(o[dt][3] / lsum)};
+      *reinterpret_cast<uint2*>(dst + 16 * dt) = make_uint2(as_u32(lo), as_u32(hi));
+    }
+    return;
+  }
+  float* mine = part + (((size_t)(m * Hkv + hk) * P + pid) * G + g) * (2 + kHeadDim);
+  if (c == 0) {
+    mine[0] = mx;
+    mine[1] = lsum;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) mine[2 + 16 * dt + 4 * c + v] = o[dt][v];
+}
+
 // fp16 GEMV for the (tied) lm_head, M <= 4: y[m][n] = fp16(sum_k x[m][k] W[n][k]), W fp16 [N][K] row-major, fp32
 // accumulation. A bandwidth kernel: the workgroup stages x[M][K] in LDS once (one barrier), then each wave streams
 // RW weight rows with 16-byte non-temporal loads (lane l takes k = 512 c + 8 l .. + 7 of chunk c, so every load is
@@ -360,10 +502,35 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, (int)blocks,
                 G, P, Hq);
 }
+// multi-token steps and prompts on MFMA: one wave per (KV head, 16 query rows, key partition); partitions while the
+// waves number fewer than kAttnMfmaTargetWaves, at most one per kAttnMinKeys of max_keys, within the workspace (each
+// wave splits the keys its rows actually attend, so a bound well above the real count costs nothing)
+hipError_t launch_attention_mfma(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M,
+                                 int Hq, int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes,
+                                 hipStream_t st) {
+  const int G = Hq / Hkv;
+  const long waves = (long)((M * G + 15) / 16) * Hkv;
+  int P = 1;
+  if (ws && waves < kAttnMfmaTargetWaves && max_keys >= 2 * kAttnMinKeys) {
+    P = (int)std::min<long>({(kAttnMfmaTargetWaves + waves - 1) / waves, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
+                             (long)kAttnMaxParts});
+    const size_t per = (size_t)M * Hkv * G * (2 + kHeadDim) * sizeof(float);
+    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, ws_bytes / per));
+  }
+  float* part = static_cast<float*>(ws);
+  hipError_t e = launch(attention_mfma, dim3((unsigned)waves, P), dim3(64), 0, st, q, k, v, pos, out, M, Hq, Hkv, L,
+                        scale, part);
+  if (e != hipSuccess || P == 1) return e;
+  const long threads = (long)M * Hq * kHeadDim;
+  return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, M * Hkv, G, P,
+                Hq);
+}
 }  // namespace
 
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
                             int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+  if ((long)M * (Hq / Hkv) >= kAttnMfmaMinRows)
+    return launch_attention_mfma(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
   if ((long)M * Hkv < 64)                                     // few tokens: one query head per block, short steps
     return launch_attention<1, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
   switch (Hq / Hkv) {

@@ -96,6 +96,10 @@ constexpr int kAttnTargetBlocks = 256;
 constexpr int kAttnMinKeys = 64;
 constexpr int kAttnMinSplitKeys = 512;
 constexpr int kAttnMaxParts = 16;
+// the MFMA attention takes steps with at least kAttnMfmaMinRows query rows (tokens x query heads per KV head), and
+// splits keys while its waves number fewer than kAttnMfmaTargetWaves
+constexpr int kAttnMfmaMinRows = 32;
+constexpr int kAttnMfmaTargetWaves = 512;
 constexpr int kAttnManyBlocks = 512;      // from this many blocks on, at most 4 waves per block
 constexpr int kMaxSplits = 32;
 constexpr size_t kCounterBytes = 16384;

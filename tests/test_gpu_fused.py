@@ -179,8 +179,11 @@ def test_qkv_rope_equals_projection_then_rope(cuda, hq, hkv, k):
 @pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
                                                 (28, 4, 300, list(range(200, 248))), (2, 1, 64, [10, 40]),
                                                 (16, 2, 4096, [4095]), (28, 4, 2048, [5, 2047]),
-                                                (16, 2, 768, list(range(512, 528)))])
+                                                (16, 2, 768, list(range(512, 528))), (16, 2, 600, list(range(100, 400))),
+                                                (12, 2, 300, list(range(0, 300, 37)))])
 def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
+    """Decode steps (a few tokens: one block per (token, head group), key partitions merged by a second launch) and
+    multi-token steps and prompts (from 32 query rows per KV head: the MFMA kernel, with and without partitions)."""
     g = torch.Generator(device="cuda").manual_seed(hq + L)
     m = len(positions)
     q = torch.randn(m, hq, 128, generator=g, device="cuda").half()
