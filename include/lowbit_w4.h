@@ -190,6 +190,23 @@ int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, i
                        const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv,
                        int64_t L, void* stream);
 
+/* The RoPE factors of a step (no counterpart in the reference; the angles of lowbit_rope_kv evaluated once per step
+ * instead of once per head and layer): table [M][64] of fp16 pairs (cos, sin) of positions[m] * inv_freq[i] (fp32
+ * angle, cos and sin in fp32 rounded to fp16, as lowbit_rope_kv computes them). */
+int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* table, int64_t M, void* stream);
+
+/* lowbit_w4_qkv_rope for M >= 1 tokens (a multi-token step or a prompt; no counterpart in the reference; it replaces
+ * lowbit_w4_linear_fused / lowbit_w4_gemm_prefill with LOWBIT_EPI_BIAS followed by lowbit_rope_kv). x [M, K] is
+ * the normalized layer input; token m's q -> q_out [M][Hq][128], its k and v -> the caches' row positions[m];
+ * rope_table is lowbit_rope_table's output for these positions. Up to 64 rows run the MFMA GEMM, more the prefill
+ * GEMM; the workspace is that kernel's (as lowbit_w4_gemm_mfma or lowbit_w4_gemm_prefill; NULL = no K split). The
+ * same bits as the unfused pair; more than 64 rows require (M + 128) * K * 2 < 2^31; the table 16-byte aligned,
+ * bias, q_out and the caches 8-byte aligned. */
+int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t M, int64_t N, int64_t K,
+                            int64_t group, const void* bias, const int64_t* positions, const void* rope_table,
+                            void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv, int64_t L,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]
  * (at most L); scores scaled by `scale`, softmax and P.V in fp32. max_keys: an upper bound on positions[m] + 1 over
  * the calls that will run (sizes the launch; a captured graph keeps it; keys past it are still attended, by the last

@@ -381,11 +381,51 @@ int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, i
              1, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
   a.epi.mode = kEpiRopeQKV;
   a.epi.aux = static_cast<const f16*>(bias);
-  a.epi.rope = RopeArgs{positions, inv_freq, static_cast<f16*>(q_out), static_cast<f16*>(k_cache),
+  a.epi.rope = RopeArgs{positions, inv_freq, nullptr, static_cast<f16*>(q_out), static_cast<f16*>(k_cache),
                         static_cast<f16*>(v_cache), (int)Hq, (int)Hkv, (int)L};
   a.norm_w = static_cast<const f16*>(norm_weight);
   a.eps = eps;
   return hip_status(gemv_mfma_layout_launch(a, 0), "w4_qkv_rope");
+}
+
+int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* table, int64_t M, void* stream) {
+  if (!positions || !inv_freq || !table) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (M < 1 || !fits_int(M * 64)) return fail(LOWBIT_ERR_SHAPE, "rope_table: M must be positive");
+  if (reinterpret_cast<uintptr_t>(table) & 3) return fail(LOWBIT_ERR_ALIGN, "rope_table needs a 4-byte aligned table");
+  if (int rc = check_device()) return rc;
+  return hip_status(rope_table_launch(positions, inv_freq, static_cast<uint32_t*>(table), (int)M,
+                                      static_cast<hipStream_t>(stream)),
+                    "rope_table");
+}
+
+int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t M, int64_t N, int64_t K,
+                            int64_t group, const void* bias, const int64_t* positions, const void* rope_table,
+                            void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv, int64_t L,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_common(x, w, s, q_out, M, N, K, group)) return rc;
+  if (M < 1) return fail(LOWBIT_ERR_ROWS, "qkv_rope_rows takes at least one row");
+  if (!bias || !positions || !rope_table || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || N != (Hq + 2 * Hkv) * 128 || !fits_int(L * 128 * Hkv) ||
+      !fits_int(M * Hq * 128))
+    return fail(LOWBIT_ERR_SHAPE, "qkv_rope: N must be (Hq + 2 Hkv) * 128 with Hkv dividing Hq, L positive");
+  if (K % 128 || group % 128) return fail(LOWBIT_ERR_LAYOUT, "the MFMA layout needs K and the group size to be multiples of 128");
+  if (int rc = check_mfma_layout_limits(N, K, group, 0)) return rc;
+  if (M > 64 && (M + 128) * K * 2 > INT_MAX) return fail(LOWBIT_ERR_SHAPE, "the prefill GEMM takes (M + 128) * K * 2 < 2^31");
+  if (!aligned16(rope_table) ||
+      ((reinterpret_cast<uintptr_t>(bias) | reinterpret_cast<uintptr_t>(q_out) | reinterpret_cast<uintptr_t>(k_cache) |
+        reinterpret_cast<uintptr_t>(v_cache)) & 7))
+    return fail(LOWBIT_ERR_ALIGN, "qkv_rope_rows needs a 16-byte aligned rope table and 8-byte aligned bias, q_out and caches");
+  if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
+    return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(q_out),
+             (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
+  a.epi.mode = kEpiRopeQKV;
+  a.epi.aux = static_cast<const f16*>(bias);
+  a.epi.rope = RopeArgs{positions, nullptr, static_cast<const uint32_t*>(rope_table), static_cast<f16*>(q_out),
+                        static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), (int)Hq, (int)Hkv, (int)L};
+  if (M <= 64) return hip_status(gemm_mfma_launch(a, 0, workspace, workspace ? workspace_bytes : 0), "w4_qkv_rope_rows");
+  return hip_status(gemm_prefill_launch(a, workspace, workspace ? workspace_bytes : 0), "w4_qkv_rope_rows");
 }
 
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,

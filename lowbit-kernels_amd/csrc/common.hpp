@@ -171,12 +171,24 @@ __device__ __forceinline__ f16 epi_value(int mode, const f16* __restrict__ aux, 
 // RoPE of one dim pair (d, d + 64) at position p as transformers computes it for fp16 models: angle =
 // fp32(p * inv_freq[d]), cos and sin in fp32 rounded to fp16, x * cos + rotate_half(x) * sin with each product and
 // the sum rounded to fp16 (no contraction)
-__device__ __forceinline__ void rope_pair(f16 x1, f16 x2, int64_t p, float inv_f, f16& o1, f16& o2) {
+__device__ __forceinline__ void rope_rotate(f16 x1, f16 x2, f16 c, f16 s, f16& o1, f16& o2) {
 #pragma clang fp contract(off)
-  const float ang = (float)p * inv_f;
-  const f16 c = (f16)cosf(ang), s = (f16)sinf(ang);
   o1 = (f16)(x1 * c) + (f16)(-x2 * s);
   o2 = (f16)(x2 * c) + (f16)(x1 * s);
+}
+
+// the fp16 cos and sin of the angle p * inv_f (fp32), as rope_pair rounds them
+__device__ __forceinline__ void rope_cos_sin(int64_t p, float inv_f, f16& c, f16& s) {
+#pragma clang fp contract(off)
+  const float ang = (float)p * inv_f;
+  c = (f16)cosf(ang);
+  s = (f16)sinf(ang);
+}
+
+__device__ __forceinline__ void rope_pair(f16 x1, f16 x2, int64_t p, float inv_f, f16& o1, f16& o2) {
+  f16 c, s;
+  rope_cos_sin(p, inv_f, c, s);
+  rope_rotate(x1, x2, c, s, o1, o2);
 }
 
 // row of head dim d (< 64: the first of the pair) in the RoPE-permuted q|k|v layout: tile d / 8, rows 0..7 hold dims
@@ -214,6 +226,13 @@ inline hipError_t launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t
                          Args... args) {
   kernel<<<grid, block, shmem, stream>>>(static_cast<KArgs>(args)...);
   return hipGetLastError();
+}
+
+// Raise a kernel's dynamic LDS limit above the default 64 KiB (gfx950 has 160 KB per CU).
+template <typename... KArgs>
+inline hipError_t allow_lds(void (*kernel)(KArgs...), size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes);
 }
 
 }  // namespace lowbit

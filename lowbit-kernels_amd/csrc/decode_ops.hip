@@ -464,6 +464,21 @@ hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, fl
   return launch(rmsnorm_kernel, dim3(M), dim3(256), 0, st, x, w, out, H, eps);
 }
 
+// table[m][i] = fp16 (cos, sin) of positions[m] * inv_freq[i] (rope_cos_sin): the RoPE factors of a step, shared by
+// every head and layer; the multi-row q|k|v GEMMs read them in their store
+__global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restrict__ pos, const float* __restrict__ inv_freq,
+                                                         uint32_t* __restrict__ table, int M) {
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= M * 64) return;
+  f16 c, s;
+  rope_cos_sin(pos[gid >> 6], inv_freq[gid & 63], c, s);
+  table[gid] = as_u32(f16x2{c, s});
+}
+
+hipError_t rope_table_launch(const int64_t* pos, const float* inv_freq, uint32_t* table, int M, hipStream_t st) {
+  return launch(rope_table_kernel, dim3((unsigned)((M * 64 + 255) / 256)), dim3(256), 0, st, pos, inv_freq, table, M);
+}
+
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
                           f16* v_cache, int M, int Hq, int Hkv, int L, bool permuted, hipStream_t st) {
   const long threads = (long)M * (Hq + 2 * Hkv) * 64;

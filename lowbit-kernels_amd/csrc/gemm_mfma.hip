@@ -48,7 +48,7 @@ constexpr int kXPitch = 256;       // bytes per staged activation row (one 128-k
 constexpr int xswz(int r) { return ((r & 3) << 2) | (r >> 2); }
 }  // namespace
 
-template <int MT, int RW, int D, int KS, int TW>
+template <int MT, int RW, int D, int KS, int TW, bool ROPE>
 __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                       const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                       int S, uint32_t* __restrict__ ctr, float* __restrict__ part,
@@ -240,6 +240,23 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   };
   if (S == 1) {
     if (kg > 0) return;
+    if constexpr (ROPE) {                                   // every tile's loads and RoPE first, the stores after
+      Out4 out[RW][MT];
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
+          const f32x4 v = acc[i][mt];                       // partner rows 8 + 4 q + v sit 32 lanes on (q + 2)
+          const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
+          out[i][mt] = q < 2 && m < M && n < N ? rope_qkv_out4(epi, m, n, v, up) : Out4{};
+        }
+#pragma unroll
+      for (int i = 0; i < RW; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) store_rope4(out[i][mt]);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < RW; ++i)
 #pragma unroll
@@ -301,7 +318,9 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   };
   for (int it = tid; it < M * nq; it += kGroupThreads * KS) {
     const int m = it / nq, n = n0 + 4 * (it - m * nq);
-    if (epi.mode == kEpiSiluMul) {
+    if constexpr (ROPE) {
+      if ((n & 15) < 8) store_rope4(rope_qkv_out4(epi, m, n, split_sum(m, n), split_sum(m, n + 8)));
+    } else if (epi.mode == kEpiSiluMul) {
       if ((n & 15) < 8) store4_silu(m, n, split_sum(m, n), split_sum(m, n + 8));
     } else {
       store4(m, n, split_sum(m, n));
@@ -319,7 +338,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
 // (the A fragments of four MFMAs, one coalesced 1 KB wave-load); its scale is row 4 (l / 16) + l % 4, broadcast
 // within the quad to the four D rows the lane holds. Rows past N, chunks past K and activation rows past M read
 // zeros through the buffer bounds.
-template <int MT, int D, int kThreads>
+template <int MT, int D, int kThreads, bool ROPE>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                         const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                         Epilogue epi) {
@@ -420,6 +439,19 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
       for (int mt = 0; mt < MT; ++mt) acc[mt] += red[((w2 - 1) * MT + mt) * 64 + lane];
   }
   // lane (r, q) holds rows n0 + 4 q + v of column m = 16 mt + r
+  if constexpr (ROPE) {                                     // every tile's loads and RoPE first, the stores after
+    Out4 out[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r, n = n0 + 4 * q;
+      const f32x4 v = acc[mt];                              // partner rows 8 + 4 q + v sit 32 lanes on (q + 2)
+      const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
+      out[mt] = q < 2 && m < M && n < N ? rope_qkv_out4(epi, m, n, v, up) : Out4{};
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) store_rope4(out[mt]);
+    return;
+  }
   const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -458,11 +490,13 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
     const int ntiles = (a.N + 15) / 16, groups = (ntiles + TW * RW - 1) / (TW * RW);
     const size_t xbytes = (size_t)KS * 2 * 16 * MT * kXPitch, redbytes = (size_t)(KS - 1) * TW * RW * MT * 1024;
     const size_t shmem = std::max(xbytes, redbytes);
-    auto kern = gemm_mfma<MT, RW, D, KS, TW>;
+    // the RoPE epilogue is its own instantiation: its registers would cost every other epilogue occupancy
+    auto kern = a.epi.mode == kEpiRopeQKV ? gemm_mfma<MT, RW, D, KS, TW, true> : gemm_mfma<MT, RW, D, KS, TW, false>;
     if (shmem > 65536) {                                     // above the default dynamic LDS limit (gfx950 has 160 KB)
-      static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
-      if (attr != hipSuccess) return attr;
+      static const hipError_t attr[2] = {allow_lds(gemm_mfma<MT, RW, D, KS, TW, false>, shmem),
+                                         allow_lds(gemm_mfma<MT, RW, D, KS, TW, true>, shmem)};
+      if (attr[0] != hipSuccess) return attr[0];
+      if (attr[1] != hipSuccess) return attr[1];
     }
     return launch(kern, dim3(groups, p.S), dim3(64 * TW * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K,
                   a.G, p.S, ctr, part, a.epi);
@@ -507,7 +541,8 @@ hipError_t launch_tiles_d(const GemvArgs& a, int waves) {
   constexpr int kThreads = 512;
   if (waves < 1 || 64 * waves > kThreads) return hipErrorInvalidConfiguration;   // never planned
   const size_t shmem = (size_t)(waves - 1) * MT * 64 * 16;
-  return launch(gemm_mfma_tiles<MT, D, kThreads>, dim3((a.N + 15) / 16), dim3(64 * waves), shmem, a.stream, a.x, a.w,
+  auto kern = a.epi.mode == kEpiRopeQKV ? gemm_mfma_tiles<MT, D, kThreads, true> : gemm_mfma_tiles<MT, D, kThreads, false>;
+  return launch(kern, dim3((a.N + 15) / 16), dim3(64 * waves), shmem, a.stream, a.x, a.w,
                 a.s, a.y, a.M, a.N, a.K, a.G, a.epi);
 }
 

@@ -37,7 +37,7 @@ __device__ __forceinline__ int swz(int row, int blk) { return row * 16 + (blk ^ 
 
 }  // namespace
 
-template <int MT, int D, int NW, int XL, int PT>
+template <int MT, int D, int NW, int XL, int PT, bool ROPE>
 __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                     const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                     int S, int MG, int items, uint32_t* __restrict__ ctr,
@@ -202,6 +202,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
     *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
   };
   if (S == 1) {
+    if constexpr (ROPE) {                                   // per tile: the MT column tiles' loads and RoPE, then stores
+#pragma unroll
+      for (int i = 0; i < PT; ++i) {
+        Out4 out[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = m0 + 16 * mt + r, n = n0 + 16 * (PT * wave + i) + 4 * q;
+          const f32x4 v = acc[i][mt];                       // partner rows 8 + 4 q + v sit 32 lanes on (q + 2)
+          const f32x4 up = {shfl_down32(v[0]), shfl_down32(v[1]), shfl_down32(v[2]), shfl_down32(v[3])};
+          out[mt] = q < 2 && m < M && n < N ? rope_qkv_out4(epi, m, n, v, up) : Out4{};
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) store_rope4(out[mt]);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < PT; ++i)
 #pragma unroll
@@ -260,7 +276,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   };
   for (int it = tid; it < mrows * nq; it += kThreads) {
     const int m = m0 + it / nq, n = n0 + 4 * (it % nq);
-    if (epi.mode == kEpiSiluMul) {
+    if constexpr (ROPE) {
+      if ((n & 15) < 8) store_rope4(rope_qkv_out4(epi, m, n, split_sum(m, n), split_sum(m, n + 8)));
+    } else if (epi.mode == kEpiSiluMul) {
       if ((n & 15) < 8) store4_silu(m, n, split_sum(m, n), split_sum(m, n + 8));
     } else {
       store4(m, n, split_sum(m, n));
@@ -276,11 +294,13 @@ hipError_t launch_prefill(const GemvArgs& a, const PrefillPlan& p, uint32_t* ctr
     return hipErrorInvalidConfiguration;                    // never planned
   } else {
   const size_t shmem = (size_t)2 * 16 * MT * 256;
-  auto kern = gemm_prefill<MT, D, NW, XL, PT>;
+  // the RoPE epilogue is its own instantiation: its registers would cost every other epilogue occupancy
+  auto kern = a.epi.mode == kEpiRopeQKV ? gemm_prefill<MT, D, NW, XL, PT, true> : gemm_prefill<MT, D, NW, XL, PT, false>;
   if (shmem > 65536) {
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
-    if (attr != hipSuccess) return attr;
+    static const hipError_t attr[2] = {allow_lds(gemm_prefill<MT, D, NW, XL, PT, false>, shmem),
+                                       allow_lds(gemm_prefill<MT, D, NW, XL, PT, true>, shmem)};
+    if (attr[0] != hipSuccess) return attr[0];
+    if (attr[1] != hipSuccess) return attr[1];
   }
   return launch(kern, dim3(p.items), dim3(64 * NW), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G, p.S, p.MG,
                 p.items, ctr, part, a.epi);

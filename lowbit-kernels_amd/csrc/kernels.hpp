@@ -11,14 +11,16 @@ namespace lowbit {
 //   kEpiResidual  y[m][n] = residual[m][n] + fp16(acc)                   (aux = residual [M][N]; may be y itself)
 //   kEpiSiluMul   rows interleaved 8 gate, 8 up per 16-row tile; y [M][N/2] = silu(fp16(gate)) * fp16(up),
 //                 output column 8 t + r for gate row 16 t + r, up row 16 t + 8 + r
-//   kEpiRopeQKV   (one row, GEMV only) the q|k|v projection of a decoder layer with its rows permuted per 128-row head
-//                 so that tile j holds dims 8 j .. 8 j + 7 and 64 + 8 j .. 64 + 8 j + 7: fp16(acc) + aux[n] (bias),
-//                 then RoPE at rope.pos[0] on q and k heads; q -> rope.q_out [Hq][128], k and v -> the caches' row
-//                 pos (as lowbit_rope_kv on the unfused, unpermuted output)
+//   kEpiRopeQKV   the q|k|v projection of a decoder layer with its rows permuted per 128-row head so that tile j
+//                 holds dims 8 j .. 8 j + 7 and 64 + 8 j .. 64 + 8 j + 7: fp16(acc) + aux[n] (bias), then RoPE at
+//                 rope.pos[m] on q and k heads; q -> rope.q_out [M][Hq][128], k and v -> the caches' row pos[m] (as
+//                 lowbit_rope_kv on the unfused output); the GEMV for one row (angles from rope.inv_freq), the MFMA
+//                 and prefill GEMMs for more (cos and sin from the table rope.cos_sin)
 enum : int { kEpiStore = 0, kEpiBias = 1, kEpiResidual = 2, kEpiSiluMul = 3, kEpiRopeQKV = 4 };
 struct RopeArgs {
   const int64_t* pos = nullptr;
-  const float* inv_freq = nullptr;
+  const float* inv_freq = nullptr;         // the GEMV's: cos and sin evaluated in its store
+  const uint32_t* cos_sin = nullptr;       // the GEMMs': the step's table [M][64] of fp16 (cos, sin) (rope_table)
   f16* q_out = nullptr;
   f16* k_cache = nullptr;
   f16* v_cache = nullptr;
@@ -29,6 +31,57 @@ struct Epilogue {
   const f16* aux = nullptr;
   RopeArgs rope;
 };
+
+// Four outputs of the kEpiRopeQKV epilogue, packed fp16, and where they go (dst == nullptr: nothing to store): dims
+// d .. d + 3 of a head in `lo`, their partners d + 64 .. d + 67 in `hi`, stored 64 values on.
+struct Out4 {
+  f16* dst = nullptr;
+  uint2 lo, hi;
+};
+
+// kEpiRopeQKV for token m of a multi-row step: rows n .. n + 3 of a 16-row tile of the RoPE-permuted q|k|v output
+// (n % 4 == 0, n % 16 < 8) with their partners n + 8 .. n + 11, fp32 sums v1 and v2: + bias, RoPE at rope.pos[m] on
+// q and k heads, q -> rope.q_out [M][Hq][128], k and v -> the caches' row pos[m] (none written outside 0..L-1). The
+// four rows are dims d .. d + 3 (d % 4 == 0) of one head, so the bias, the (cos, sin) pairs and each output half move
+// as one vector (the entry point checks the 8- and 16-byte alignments). cos and sin come from the step's table: the
+// angle of (token, dim) is the same in every head and layer, and evaluating it here would leave 4 sin + cos per 16
+// tokens to each lane of a tile at the kernel's end. The same roundings as the bias epilogue followed by
+// lowbit_rope_kv on the permuted output.
+__device__ __forceinline__ Out4 rope_qkv_out4(const Epilogue& e, int m, int n, const f32x4& v1, const f32x4& v2) {
+  const RopeArgs& ra = e.rope;
+  Out4 o;
+  const int64_t p = ra.pos[m];
+  if (p < 0 || p >= ra.L) return o;
+  const int hh = n >> 7, pj = n & 127, d = 8 * (pj >> 4) + (pj & 7);
+  const uint2 b1 = *reinterpret_cast<const uint2*>(e.aux + n), b2 = *reinterpret_cast<const uint2*>(e.aux + n + 8);
+  const f16x2 b[4] = {as_f16x2(b1.x), as_f16x2(b1.y), as_f16x2(b2.x), as_f16x2(b2.y)};
+  f16 x1[4], x2[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x1[i] = (f16)v1[i] + b[i >> 1][i & 1];
+    x2[i] = (f16)v2[i] + b[2 + (i >> 1)][i & 1];
+  }
+  if (hh >= ra.Hq + ra.Hkv) {
+    o.dst = ra.v_cache + ((size_t)(hh - ra.Hq - ra.Hkv) * ra.L + p) * 128 + d;
+  } else {
+    const u32x4 cs = *reinterpret_cast<const u32x4*>(ra.cos_sin + (size_t)m * 64 + d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 c_s = as_f16x2(cs[i]);
+      rope_rotate(x1[i], x2[i], c_s[0], c_s[1], x1[i], x2[i]);
+    }
+    o.dst = hh < ra.Hq ? ra.q_out + ((size_t)m * ra.Hq + hh) * 128 + d : ra.k_cache + ((size_t)(hh - ra.Hq) * ra.L + p) * 128 + d;
+  }
+  o.lo = make_uint2(as_u32(f16x2{x1[0], x1[1]}), as_u32(f16x2{x1[2], x1[3]}));
+  o.hi = make_uint2(as_u32(f16x2{x2[0], x2[1]}), as_u32(f16x2{x2[2], x2[3]}));
+  return o;
+}
+
+__device__ __forceinline__ void store_rope4(const Out4& o) {
+  if (!o.dst) return;
+  *reinterpret_cast<uint2*>(o.dst) = o.lo;
+  *reinterpret_cast<uint2*>(o.dst + 64) = o.hi;
+}
 
 struct GemvArgs {
   const f16* x;
@@ -139,6 +192,7 @@ constexpr bool prefill_fits(int MT, int D, int NW, int XL) {
 PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes);
 hipError_t gemm_prefill_launch(const GemvArgs& a, void* workspace, size_t workspace_bytes);
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st);
+hipError_t rope_table_launch(const int64_t* pos, const float* inv_freq, uint32_t* table, int M, hipStream_t st);
 hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_freq, f16* q_out, f16* k_cache,
                           f16* v_cache, int M, int Hq, int Hkv, int L, bool permuted, hipStream_t st);
 hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st);

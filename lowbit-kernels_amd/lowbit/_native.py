@@ -44,6 +44,9 @@ SIGNATURES = {
     "lowbit_rope_kv": ([_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp], _int),
     "lowbit_w4_qkv_rope": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _i64,
                             _i64, _i64, _vp], _int),
+    "lowbit_rope_table": ([_vp, _vp, _vp, _i64, _vp], _int),
+    "lowbit_w4_qkv_rope_rows": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                 _i64, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
@@ -416,6 +419,43 @@ class NativeExt:
                                               ptr(nw) if nw is not None else None, float(eps), ptr(positions),
                                               ptr(inv_freq), ptr(q_out), ptr(k_cache), ptr(v_cache), hq, hkv,
                                               k_cache.shape[1], _stream(x.device)))
+
+    def rope_table(self, positions, inv_freq, out=None):
+        """The RoPE factors of a step: int32 [M, 64], each the fp16 pair (cos, sin) of positions[m] * inv_freq[i], as
+        lowbit_rope_kv evaluates them (w4_qkv_rope_rows reads it)."""
+        import torch
+        m = positions.shape[0]
+        _need(positions, "positions", torch.int64, (m,), positions.device)
+        _need(inv_freq, "inv_freq", torch.float32, (64,), positions.device)
+        t = out if out is not None else torch.empty(m, 64, dtype=torch.int32, device=positions.device)
+        _need(t, "out", torch.int32, (m, 64), positions.device)
+        with _DeviceGuard(positions.device):
+            check(self.lib.lowbit_rope_table(ptr(positions), ptr(inv_freq), ptr(t), m, _stream(positions.device)))
+        return t
+
+    def w4_qkv_rope_rows(self, x, w, s, group, bias, positions, table, q_out, k_cache, v_cache, hq, hkv):
+        """M tokens: the RoPE-permuted q|k|v projection of the normalized input x [M, K] (+ bias, RoPE, cache write)
+        into q_out [M, Hq, 128] and the caches [Hkv, L, 128] at rows positions[m]; table = rope_table(positions, ...)
+        (the MFMA GEMM up to 64 rows, the prefill GEMM beyond, each with its own workspace)."""
+        import torch
+        _check_tensors(x, w, s, group)
+        m = x.shape[0]
+        if w.shape[0] != (hq + 2 * hkv) * 128:
+            raise RuntimeError("the q|k|v weight must have (Hq + 2 Hkv) * 128 rows")
+        _need(bias, "bias", torch.float16, (w.shape[0],), x.device)
+        _need(table, "table", torch.int32, (m, 64), x.device)
+        if k_cache.dim() != 3:
+            raise RuntimeError("the caches must be [Hkv, L, 128]")
+        _need(positions, "positions", torch.int64, (m,), x.device)
+        _need(q_out, "q_out", torch.float16, (m, hq, 128), x.device)
+        _need(k_cache, "k_cache", torch.float16, (hkv, k_cache.shape[1], 128), x.device)
+        _need(v_cache, "v_cache", torch.float16, tuple(k_cache.shape), x.device)
+        with _DeviceGuard(x.device):
+            st = _stream(x.device)
+            ws = workspace(x.device, st, WORKSPACE_BYTES if m <= 64 else PREFILL_WORKSPACE_BYTES)
+            check(self.lib.lowbit_w4_qkv_rope_rows(ptr(x), ptr(w), ptr(s), m, w.shape[0], x.shape[1], group, ptr(bias),
+                                                   ptr(positions), ptr(table), ptr(q_out), ptr(k_cache), ptr(v_cache),
+                                                   hq, hkv, k_cache.shape[1], ptr(ws), ws.numel(), st))
 
     def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale, split=True):
         """split=False runs one block per (token, head group), without the key partitions and their workspace."""

@@ -168,11 +168,22 @@ class FusedQwen2:
         q = torch.empty(m, self.hq, self.head_dim, dtype=torch.float16, device=h.device)
         attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
         fuse = m == 1 and self.quant == "int4" and self.hidden <= 16384
+        # more rows: the int4 GEMM that lay["qkv"] would pick (the MFMA GEMM up to 64 rows, the prefill GEMM where
+        # prefill_path sends them) takes the RoPE epilogue too, its cos and sin from one table per step;
+        # dequantize + BLAS keeps the separate rope_kv
+        rope_rows = (not fuse and self.quant == "int4" and
+                     (m <= 64 or ops.prefill_path(m, self.layers[0]["qkv"].wq)) if self.layers else False)
+        table = ext.rope_table(positions, self.inv_freq) if rope_rows else None
         for i, lay in enumerate(self.layers):
             if fuse:                                          # RMSNorm in the prologue, RoPE + cache write in the store
                 wq = lay["qkv"].wq
                 ext.w4_qkv_rope(h, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, self.inv_freq, q,
                                 self.k_cache[i], self.v_cache[i], self.hq, self.hkv, norm=(lay["in_norm"], self.eps))
+            elif rope_rows:                                   # RoPE + cache write in the GEMM's store
+                ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
+                wq = lay["qkv"].wq
+                ext.w4_qkv_rope_rows(xn, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, table, q,
+                                     self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
             else:
                 ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
                 qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)

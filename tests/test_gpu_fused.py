@@ -3,6 +3,8 @@
   then the torch add); silu-mul equals torch's silu(gate) * up on the unfused outputs; GEMV (M = 1) and MFMA paths,
   with and without the split of K;
 * lowbit_rmsnorm and lowbit_rope_kv against transformers' own Qwen2RMSNorm and apply_rotary_pos_emb;
+* lowbit_w4_qkv_rope (one row) and lowbit_w4_qkv_rope_rows with lowbit_rope_table (M rows) bit for bit against the
+  projection with the bias epilogue followed by lowbit_rope_kv;
 * lowbit_attention against an fp32 causal softmax attention;
 * FusedQwen2 (fp16 and int4) against the transformers model on the same tokens."""
 import math
@@ -174,6 +176,74 @@ def test_qkv_rope_equals_projection_then_rope(cuda, hq, hkv, k):
             assert torch.equal(a, b), p
         if p >= L:                                          # out of the cache: nothing written, q untouched
             assert int(torch.count_nonzero(caches[1][1])) == 0 and int(torch.count_nonzero(caches[1][0])) == 0
+
+
+def test_rope_table_holds_the_factors_rope_kv_applies(cuda):
+    """lowbit_rope_table's (cos, sin) are exactly the factors lowbit_rope_kv multiplies by: with x = 1 and its
+    partner 0, rope_kv's rotated pair is (fp16(1 * cos) - fp16(0 * sin), fp16(0 * cos) + fp16(1 * sin)) = (cos, sin)
+    bit for bit. Also within an fp16 ulp of torch's fp32 cos and sin (torch's fp32 functions may differ from the
+    device library's in the last fp32 bit, which can move an fp16 rounding)."""
+    hq, hkv, L = 2, 1, 70000
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    pos = torch.tensor([0, 1, 37, 4095, 32767, 65535, 69999], device="cuda")
+    m = pos.shape[0]
+    table = ops.ext().rope_table(pos, inv_freq)
+    qkv = torch.zeros(m, (hq + 2 * hkv) * 128, dtype=torch.half, device="cuda")
+    qkv.view(m, hq + 2 * hkv, 128)[:, :, :64] = 1
+    q = torch.zeros(m, hq, 128, dtype=torch.half, device="cuda")
+    kc = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+    ops.ext().rope_kv(qkv, pos, inv_freq, q, kc, torch.zeros_like(kc), hq, hkv)
+    cs = table.view(torch.int16).view(m, 64, 2).view(torch.half)
+    assert torch.equal(cs[:, :, 0], q[:, 0, :64]) and torch.equal(cs[:, :, 1], q[:, 0, 64:])
+    ang = pos.float()[:, None] * inv_freq[None, :]
+    assert ulp_diff(cs[:, :, 0].contiguous(), torch.cos(ang).half()) <= 1
+    assert ulp_diff(cs[:, :, 1].contiguous(), torch.sin(ang).half()) <= 1
+
+
+@pytest.mark.parametrize("hq,hkv,k", [(2, 1, 256), (16, 2, 2048), (28, 4, 3584)])
+@pytest.mark.parametrize("m", [2, 16, 48, 64, 130, 512])
+def test_qkv_rope_rows_equal_projection_then_rope(cuda, hq, hkv, k, m):
+    """lowbit_w4_qkv_rope_rows (M tokens: q|k|v GEMM, bias, RoPE from the step's table, cache write in one launch;
+    the MFMA GEMM up to 64 rows, the prefill GEMM beyond) gives the same bits as the same GEMM with the bias epilogue
+    followed by lowbit_rope_kv on the permuted layout, on the automatic plan and with K split in two and four (both
+    sides run the same plan; the split fixup pairs rows r and r + 8 of a tile). Tokens at positions outside the
+    cache write nothing, their q included."""
+    n, L = (hq + 2 * hkv) * 128, 600
+    wq, _, *_, gen = make_weight(k, n, 3 * k + n + m, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    x = (torch.randn(m, k, generator=gen) * 3).half().cuda()
+    pos = torch.randperm(L, generator=gen)[:m]
+    pos[m // 2] = L + 3                                     # one token outside the cache
+    pos = pos.cuda()
+    table = ext.rope_table(pos, inv_freq)
+    for s in (0, 2, 4):
+        outs = []
+        for fused_call in (False, True):
+            q = torch.zeros(m, hq, 128, dtype=torch.half, device="cuda")
+            kc = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+            vc = torch.zeros_like(kc)
+            _native.check(_native.lib().lowbit_set_launch_override(0, 0, s))
+            try:
+                if fused_call:
+                    ext.w4_qkv_rope_rows(x, wq.packed_mma, wq.scales, wq.group, bias, pos, table, q, kc, vc, hq, hkv)
+                elif m <= 64:
+                    qkv = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias)
+                else:
+                    qkv = ext.w4_gemm_prefill(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias)
+            finally:
+                _native.check(_native.lib().lowbit_set_launch_override(0, 0, 0))
+            if not fused_call:
+                ext.rope_kv(qkv, pos, inv_freq, q, kc, vc, hq, hkv, permuted=True)
+            outs.append((q, kc, vc))
+        for a, b in zip(*outs):
+            assert torch.equal(a, b), (m, s)
+        assert int(torch.count_nonzero(outs[1][0][m // 2])) == 0
+        written = torch.zeros(L, dtype=torch.bool, device="cuda")
+        written[pos[pos < L]] = True
+        assert int(torch.count_nonzero(outs[1][1][:, ~written])) == 0
+        assert int(torch.count_nonzero(outs[1][1][:, written])) > outs[1][1][:, written].numel() * 0.99
 
 
 @pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
