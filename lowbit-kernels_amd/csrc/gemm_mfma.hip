@@ -503,7 +503,13 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
   }
 }
 
-// K-groups of 3, 5, 6 or 8 tile-waves are built with one tile per wave and 2 ring slots only
+// K-groups of 3, 5, 6 or 8 tile-waves are built with one tile per wave and 2 ring slots (3 also for 5 and 6)
+template <int MT, int D>
+hipError_t dispatch_wide56(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part, int ks) {
+  if (p.KW == 5) return ks == 1 ? launch_gemm<MT, 1, D, 1, 5>(a, p, ctr, part) : launch_gemm<MT, 1, D, 2, 5>(a, p, ctr, part);
+  return ks == 1 ? launch_gemm<MT, 1, D, 1, 6>(a, p, ctr, part) : launch_gemm<MT, 1, D, 2, 6>(a, p, ctr, part);
+}
+
 template <int MT>
 hipError_t dispatch_wide(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, float* part) {
   const int ks = p.waves / p.KW;
@@ -511,8 +517,8 @@ hipError_t dispatch_wide(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
     case 3:
       return ks == 1 ? launch_gemm<MT, 1, 2, 1, 3>(a, p, ctr, part)
            : ks == 2 ? launch_gemm<MT, 1, 2, 2, 3>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 4, 3>(a, p, ctr, part);
-    case 5: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 5>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 5>(a, p, ctr, part);
-    case 6: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 6>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 6>(a, p, ctr, part);
+    case 5:
+    case 6: return p.D == 3 ? dispatch_wide56<MT, 3>(a, p, ctr, part, ks) : dispatch_wide56<MT, 2>(a, p, ctr, part, ks);
     default: return ks == 1 ? launch_gemm<MT, 1, 2, 1, 8>(a, p, ctr, part) : launch_gemm<MT, 1, 2, 2, 8>(a, p, ctr, part);
   }
 }
@@ -587,7 +593,8 @@ int tiles_ring(int MT) { return MT <= 2 ? 4 : MT == 3 ? 3 : 2; }
 // M = 16..64: 3584 x 18944 with 237 workgroups of 5, M = 64 29.3 -> 23.0 us, M = 32 18.7 -> 14.1; 2048 x 22016 with
 // 230 of 6, M = 64 18.7 -> 15.2; 1536 x 17920 with 224 of 5, M = 64 15.0 -> 12.5). Past 2048 tiles, up to 48 rows, the
 // count that leaves the fewest tiles per CU, (workgroups / 256 rounded up) x tile-waves (3584 x 37888: 5, M = 32
-// 27.9 -> 23.2 us); at 64 rows those layers keep 4 (5 is 10% slower there). Up to 16 rows a layer of 385 to 768
+// 27.9 -> 23.2 us); at 64 rows those layers take 6 with one K-group (3584 x 37888: 39.4 us with 4, 38.4 with 5 and
+// 2 K-groups, 34.4 with 6 and 1; 35.0 vs 39.6 for 4 in an earlier sweep). Up to 16 rows a layer of 385 to 768
 // tiles takes 3, so that its 129-256 workgroups occupy more CUs than the 97-192 of 4 (2048 x 11008: 6.82 -> 6.46 us;
 // 1536 x 8960: 6.04 -> 5.78); from 17 rows 4 is level or up to 3% faster.
 int balanced_tile_waves(int ntiles, int MT) {
@@ -596,7 +603,7 @@ int balanced_tile_waves(int ntiles, int MT) {
   if (ntiles <= kW * kCUs) return kW;
   for (int tw : {5, 6, 8})
     if ((ntiles + tw - 1) / tw <= kCUs) return tw;
-  if (MT > 3) return kW;
+  if (MT > 3) return 6;
   int best = kW;
   long best_tiles = (long)((ntiles + kW - 1) / kW + kCUs - 1) / kCUs * kW;
   for (int tw : {5, 6, 8}) {
@@ -660,7 +667,13 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   }
   while (ks > 1 && ks * S > KC) ks /= 2;
   p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);
-  if (KW != kW) p.D = 2;
+  // 5 or 6 tile-waves: 2 slots, or 3 on one round of workgroups with 2 K-groups of at least 12 chunks each up to 32
+  // rows (MI355X graph sweep, 3584 x 18944: M = 16 11.64 -> 11.46 us, M = 32 14.11 -> 13.84; at 48 and 64 rows, and on
+  // 1536 x 17920, 2048 x 22016 and the two-round 3584 x 37888, the third slot costs 1-3%)
+  if (KW != kW) {
+    const bool deep = p.MT <= 2 && ks == 2 && groups <= 256 && KC >= 24 && (KW == 5 || KW == 6);
+    p.D = o.ring == 2 || o.ring == 3 ? (o.ring == 3 && (KW == 5 || KW == 6) ? 3 : 2) : (deep ? 3 : 2);
+  }
   while (!gemm_fits(p.MT, p.R, p.D, ks, KW)) {              // fewer K-groups, then fewer slots, then fewer tiles
     if (ks > 1) ks /= 2;
     else if (p.D > 2) --p.D;

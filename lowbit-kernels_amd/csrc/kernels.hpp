@@ -162,7 +162,7 @@ constexpr size_t kCounterBytes = 16384;
 // are built with one tile per wave and 2 slots, at most 2 K-groups (4 of 3 tile-waves up to 32 rows).
 constexpr bool gemm_fits(int MT, int RW, int D, int KS, int TW = 4) {
   if (TW == 3) return RW == 1 && D == 2 && (KS <= 2 || MT <= 2);
-  if (TW != 4) return RW == 1 && D == 2 && KS <= 2 && (TW * KS <= 12 || MT <= 3);
+  if (TW != 4) return RW == 1 && (D == 2 || (D == 3 && (TW == 5 || TW == 6))) && KS <= 2 && (TW * KS <= 12 || MT <= 3);
   if (KS == 4) return D == 2 ? (RW == 1 ? MT <= 3 : MT <= 2) : (RW == 1 && MT == 1);
   if (KS == 2) return !((RW == 2 && (MT >= 3 ? D >= 3 : (MT == 2 && D == 4))) || (MT == 4 && RW == 1 && D == 4));
   return true;

@@ -22,7 +22,7 @@ def fits(mt, rw, d, ks, tw=4):
     if tw == 3:
         return rw == 1 and d == 2 and (ks <= 2 or mt <= 2)
     if tw != 4:
-        return rw == 1 and d == 2 and ks <= 2 and (tw * ks <= 12 or mt <= 3)
+        return rw == 1 and (d == 2 or (d == 3 and tw in (5, 6))) and ks <= 2 and (tw * ks <= 12 or mt <= 3)
     if ks == 4:
         return (mt <= 3 if rw == 1 else mt <= 2) if d == 2 else (rw == 1 and mt == 1)
     if ks == 2:
@@ -76,9 +76,10 @@ def test_every_launch_shape_against_fp64(cuda, k, n):
 
 @pytest.mark.parametrize("k,n", [(1024, 16 * 37 + 5), (3584, 4096), (2048, 16 * 101)])
 def test_k_group_widths_give_the_bits_of_four_tile_waves(cuda, k, n):
-    """K-groups of 3, 5, 6 or 8 tile-waves (one tile per wave) compute every tile as K-groups of 4 do: the same chunks
-    per K-group in the same order, so the bits are the same, with and without a K split. The tile counts leave a
-    partial last workgroup, and 16 M rows over 3, 5 or 6 waves a partial last round of x staging."""
+    """K-groups of 3, 5, 6 or 8 tile-waves (one tile per wave; 5 and 6 also with a 3-slot ring) compute every tile as
+    K-groups of 4 do: the same chunks per K-group in the same order, so the bits are the same, with and without a K
+    split. The tile counts leave a partial last workgroup, and 16 M rows over 3, 5 or 6 waves a partial last round of
+    x staging."""
     wq, ref_w, *_, gen = make_weight(k, n, k + n, layouts=("mma",))
     ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     for m in (1, 16, 17, 40, 64):
@@ -93,17 +94,19 @@ def test_k_group_widths_give_the_bits_of_four_tile_waves(cuda, k, n):
                 base = gemm(x, wq, 1, 2, splits, ws, ks, tw=4)
                 assert rel(base, ref) <= lim, (k, n, m, ks, splits)
                 for tw in (3, 5, 6, 8):
-                    if not fits(mt, 1, 2, ks, tw):
-                        continue
-                    y = gemm(x, wq, 1, 2, splits, ws, ks, tw)
-                    assert torch.equal(y, base), (k, n, m, ks, splits, tw)
+                    for d in (2, 3):
+                        if not fits(mt, 1, d, ks, tw):
+                            continue
+                        y = gemm(x, wq, 1, d, splits, ws, ks, tw)
+                        assert torch.equal(y, base), (k, n, m, ks, splits, tw, d)
     torch.cuda.synchronize()
     assert int(torch.count_nonzero(ws[:_native.WORKSPACE_COUNTER_BYTES])) == 0
 
 
 def test_automatic_tile_waves_balance_the_rounds(cuda):
     """Past 1024 tiles the planner takes the fewest tile-waves that fit one round of workgroups (3584 x 18944: 1184
-    tiles -> 237 workgroups of 5, with 2 K-groups); the result equals that launch forced, bit for bit."""
+    tiles -> 237 workgroups of 5, with 2 K-groups; a 3-slot ring at 24 rows, 2 at 64); the result equals that launch
+    forced with 2 slots, bit for bit (the ring depth does not change the order of the chunks)."""
     wq, ref_w, *_, gen = make_weight(3584, 18944, 7, layouts=("mma",))
     ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     for m in (24, 64):
