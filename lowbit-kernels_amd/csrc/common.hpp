@@ -153,6 +153,25 @@ __device__ __forceinline__ uint16_t buffer_load2_nt(__amdgpu_buffer_rsrc_t rsrc,
   return __builtin_bit_cast(uint16_t, __builtin_amdgcn_raw_buffer_load_b16(rsrc, offset, 0, kNonTemporal));
 }
 
+// Split-K partial sums handed from one workgroup to another: buffer stores and loads with the sc1 cache-policy bit,
+// which on gfx950 makes each access coherent across the XCDs' L2 caches by itself (the LLVM AMDGPU memory model
+// implements relaxed agent-scope atomic stores and loads as exactly these accesses, 4 or 8 bytes wide; here 16). So
+// once a writer has waited for its stores' acknowledgements, its arrival can be counted with a relaxed atomic: no
+// release (an L2 write-back in every split workgroup) and no acquire (an L2 invalidate in the last one).
+constexpr int kAgentCoherent = 16;         // gfx94x/gfx950 cache policy bit sc1
+__device__ __forceinline__ void store_partial4(__amdgpu_buffer_rsrc_t r, int offset, const f32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, offset, 0, kAgentCoherent);
+}
+__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, int offset, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, offset, 0, kAgentCoherent);
+}
+__device__ __forceinline__ f32x4 load_partial4(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kAgentCoherent));
+}
+__device__ __forceinline__ float load_partial(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kAgentCoherent));
+}
+
 __device__ __forceinline__ u32x4 load_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }

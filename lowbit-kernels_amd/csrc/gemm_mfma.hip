@@ -25,10 +25,11 @@
 // the K-groups are summed through LDS.
 //
 // Narrow N cannot fill 256 CUs with row groups alone, so K is also split over S workgroups per row group (grid.y)
-// when the caller passes a workspace. Each writes its fp32 partial sums; one thread per workgroup then makes them
-// visible and counts the arrival (release), and the last to arrive (acquire) adds the S partials in split order,
-// writes y and resets the counter to 0. Results do not depend on timing.
+// when the caller passes a workspace. Each writes its fp32 partial sums as agent-coherent stores (store_partial), waits
+// for them, and one thread per workgroup counts the arrival; the last to arrive reads the S partials the same way,
+// adds them in split order, writes y and resets the counter to 0. Results do not depend on timing.
 #include <algorithm>
+#include <climits>
 
 #include "kernels.hpp"
 
@@ -273,7 +274,9 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
       }
     return;
   }
-  float* mine = part + (size_t)split * M * N;               // [S][M][N] fp32
+  // [S][M][N] fp32 partials, byte offsets into the workspace (S M N 4 bytes, within the 32-bit range the planner keeps)
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)((size_t)S * M * N * 4));
+  auto poff = [&](int k, int m, int n) { return (int)((((size_t)k * M + m) * N + n) * 4); };
 #pragma unroll
   for (int i = 0; i < RW; ++i)
 #pragma unroll
@@ -281,38 +284,39 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
       const int m = 16 * mt + r, n = n0 + 16 * (tw * RW + i) + 4 * q;
       if (kg > 0 || m >= M || n >= N) continue;
       const f32x4 v = acc[i][mt];
-      float* dst = mine + (size_t)m * N + n;
+      const int off = poff(split, m, n);
       if (vec) {
-        *reinterpret_cast<f32x4*>(dst) = v;
+        store_partial4(pr, off, v);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < N) dst[e] = v[e];
+          if (n + e < N) store_partial(pr, off + 4 * e, v[e]);
       }
     }
-  // the barrier orders every wave's partial stores before thread 0's release; only the last arrival acquires, so the
-  // other workgroups keep their caches
-  __builtin_amdgcn_s_waitcnt(0);
+  // every wave waits for its partials' acknowledgements before the barrier, so thread 0 counts the workgroup's
+  // arrival only once all of them are visible to every XCD
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);                 // the partials' stores stay before the wait
+  __builtin_amdgcn_s_waitcnt(0);                            // every partial acknowledged: visible to all XCDs
   __builtin_amdgcn_s_barrier();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(ctr + grp, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(ctr + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (uint32_t)(S - 1);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);                 // the partials' loads stay after the count
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (tid == 0) __hip_atomic_store(ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nrows = min(16 * T, N - n0), nq = (nrows + 3) >> 2;
   auto split_sum = [&](int m, int n) {                      // partials of rows n .. n + 3, added in split order
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
     if ((N & 3) == 0) {
-      for (int sp = 0; sp < S; ++sp) sum += *reinterpret_cast<const f32x4*>(part + ((size_t)sp * M + m) * N + n);
+      for (int sp = 0; sp < S; ++sp) sum += load_partial4(pr, poff(sp, m, n));
     } else {
       for (int sp = 0; sp < S; ++sp)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < N) sum[e] += part[((size_t)sp * M + m) * N + n + e];
+          if (n + e < N) sum[e] += load_partial(pr, poff(sp, m, n) + 4 * e);
     }
     return sum;
   };
@@ -330,8 +334,8 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
 
 // gemm_mfma_tiles: the same MFMA arithmetic with one 16-row tile per workgroup, for M <= 64 on attention-sized layers
 // (few tiles, short K; the selection rule is tiles_win below). The row-group kernel above stages activations for 64
-// rows with a barrier per chunk and, on narrow layers, splits K over workgroups that each pay an agent-scope release to
-// add the partials; here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
+// rows with a barrier per chunk and, on narrow layers, splits K over workgroups that hand their partials over through
+// memory; here the workgroup's waves split the tile's 128-k chunks round-robin and are summed through LDS at
 // the end, so no workgroup waits for another. Each wave loads, next to its weight piece, the activation piece its B
 // fragments need (lane l: 64 contiguous bytes, x row 16 mt + l % 16, k = 128 c + 32 (l / 16) + [0, 32)) straight into
 // registers: no staging buffer and no barrier inside the K loop. Lane l's weight piece is row l % 16, quarter l / 16
@@ -642,7 +646,9 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   if (p.R == 1) p.KW = o.tile_waves > 0 ? o.tile_waves : balanced_tile_waves(ntiles, p.MT);
   const int KW = p.KW;
   const int groups = (ntiles + KW * p.R - 1) / (KW * p.R);
-  const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
+  // the partials are addressed with 32-bit byte offsets (a buffer resource): at most 2^31 - 1 bytes of them
+  const size_t part_bytes = std::min<size_t>(workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0,
+                                             (size_t)INT_MAX);
   int S = 1;
   if (o.splits > 0) {
     S = o.splits;

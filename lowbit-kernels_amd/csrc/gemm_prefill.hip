@@ -22,9 +22,10 @@
 // Work items (tile = 256 rows x 16 MT activation rows, times S splits of K) are numbered with the split fastest, then
 // the activation group, then the row group, and the workgroup -> item map puts consecutive items on the same XCD
 // (workgroup i runs on XCD i % 8), so the workgroups that share weight rows share that XCD's L2. With S > 1 each
-// workgroup writes fp32 partials to the workspace; the last to arrive (release / acquire on a per-tile counter) adds
-// them in split order, applies the epilogue and resets the counter, as in the skinny kernel.
+// workgroup writes fp32 partials to the workspace (agent-coherent stores); the last to arrive on a per-tile counter
+// adds them in split order, applies the epilogue and resets the counter, as in the skinny kernel.
 #include <algorithm>
+#include <climits>
 
 #include "kernels.hpp"
 
@@ -234,43 +235,46 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
       }
     return;
   }
-  float* mine = part + (size_t)sp * M * N;                  // [S][M][N] fp32
+  // [S][M][N] fp32 partials, byte offsets into the workspace (S M N 4 bytes, within the 32-bit range the planner keeps)
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)((size_t)S * M * N * 4));
+  auto poff = [&](int k, int m, int n) { return (int)((((size_t)k * M + m) * N + n) * 4); };
 #pragma unroll
   for (int i = 0; i < PT; ++i)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = m0 + 16 * mt + r, n = n0 + 16 * (PT * wave + i) + 4 * q;
       if (m >= M || n >= N) continue;
-      float* dst = mine + (size_t)m * N + n;
+      const int off = poff(sp, m, n);
       if (vec) {
-        *reinterpret_cast<f32x4*>(dst) = acc[i][mt];
+        store_partial4(pr, off, acc[i][mt]);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < N) dst[e] = acc[i][mt][e];
+          if (n + e < N) store_partial(pr, off + 4 * e, acc[i][mt][e]);
       }
     }
-  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);                 // the partials' stores stay before the wait
+  __builtin_amdgcn_s_waitcnt(0);                            // every partial acknowledged: visible to all XCDs
   __builtin_amdgcn_s_barrier();
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(ctr + tile, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(ctr + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == (uint32_t)(S - 1);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);                 // the partials' loads stay after the count
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   if (tid == 0) __hip_atomic_store(ctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nrows = min(kRows, N - n0), nq = (nrows + 3) >> 2, mrows = min(16 * MT, M - m0);
   auto split_sum = [&](int m, int n) {                      // partials of rows n .. n + 3, added in split order
     f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
     if ((N & 3) == 0) {
-      for (int k = 0; k < S; ++k) sum += *reinterpret_cast<const f32x4*>(part + ((size_t)k * M + m) * N + n);
+      for (int k = 0; k < S; ++k) sum += load_partial4(pr, poff(k, m, n));
     } else {
       for (int k = 0; k < S; ++k)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (n + e < N) sum[e] += part[((size_t)k * M + m) * N + n + e];
+          if (n + e < N) sum[e] += load_partial(pr, poff(k, m, n) + 4 * e);
     }
     return sum;
   };
@@ -355,7 +359,9 @@ PrefillPlan plan_gemm_prefill(int M, int N, int K, size_t workspace_bytes) {
     while (p.PT > 1 && groups(p.PT) < 2 * kPrefillTargetGroups) p.PT /= 2;
   }
   const long tiles = groups(p.PT);
-  const size_t part_bytes = workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0;
+  // the partials are addressed with 32-bit byte offsets (a buffer resource): at most 2^31 - 1 bytes of them
+  const size_t part_bytes = std::min<size_t>(workspace_bytes > kCounterBytes ? workspace_bytes - kCounterBytes : 0,
+                                             (size_t)INT_MAX);
   int S = 1;
   if (o.splits > 0) {
     S = o.splits;
