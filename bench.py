@@ -86,10 +86,11 @@ def parse():
                          "give the spread")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles", "tilewaves"], default=None,
+    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles", "tilewaves", "splits"], default=None,
                     help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
                          "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32; "
-                         "tilewaves: the row groups' tile-waves and K-groups on layers of 560 to 2368 tiles")
+                         "tilewaves: the row groups' tile-waves and K-groups on layers of 560 to 2368 tiles; "
+                         "splits: the row groups' K split x K-groups on the decode projections, M=16..64")
     ap.add_argument("--e2e", choices=["tiny", "1.5b", "3b"], default=None,
                     help="hipGraph batch-1 decode of a random-init Qwen2.5 model: fp16 vs fake-quant vs W4Linear")
     ap.add_argument("--decode-trace", choices=["hf_fp16", "hf_int4", "fused_fp16", "fused_int4"], default=None,
@@ -683,6 +684,43 @@ def sweep_tilewaves(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+def sweep_splits(a):
+    """MFMA GEMM (v5) on the 1.5B / 3B / 7B decode projections, M in {16, 32, 48, 64}: graph-timed us per call of the
+    automatic plan, of one tile per workgroup (lowbit_set_gemm_kernel(2)) and of the row groups
+    (lowbit_set_gemm_kernel(1)) with every K split S in {1, 2, 4, 8} x K-groups ks in {1, 2, 4} forced through
+    lowbit_set_launch_override(4 ks, 0, S), the rest automatic."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in ((1536, 2048), (1536, 1536), (2048, 2560), (2048, 2048), (3584, 3584), (3584, 512), (2048, 256),
+                 (1536, 256), (3584, 4608), (8960, 1536), (11008, 2048), (18944, 3584)):
+        cl = cloned_copies(torch, ops, k, n, gib=0.5)
+        for m in (16, 32, 48, 64):
+            x = torch.randn(m, k, device="cuda").half()
+            t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5), max(200, len(cl))), 2)
+            r = {"K": k, "N": n, "M": m, "auto": t()}
+            try:
+                _native.check(lib.lowbit_set_gemm_kernel(2))
+                r["tiles"] = t()
+                _native.check(lib.lowbit_set_gemm_kernel(1))
+                for sp in (1, 2, 4, 8):
+                    for ks in (1, 2, 4):
+                        if sp * ks <= k // 128:
+                            _native.check(lib.lowbit_set_launch_override(4 * ks, 0, sp))
+                            r[f"s{sp}k{ks}"] = t()
+            finally:
+                _native.check(lib.lowbit_set_gemm_kernel(0))
+                _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+            rows.append(r)
+            print(json.dumps(r), flush=True)
+        del cl
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
 def sweep_prefill(a):
     """Prefill, M in {128, 256, 512, 2048} on the Qwen2.5-3B layer (merged q|k|v and gate|up, o, down) and the 7B MLP
     projections: us/call of dequantize + hipBLASLt, fp16 hipBLASLt, the int4 prefill GEMM (automatic launch plan), the
@@ -980,6 +1018,8 @@ def main():
         sweep_tiles(a)
     elif a.sweep == "tilewaves":
         sweep_tilewaves(a)
+    elif a.sweep == "splits":
+        sweep_splits(a)
     elif a.e2e and a.decode_trace:
         decode_trace(a)
     elif a.e2e:

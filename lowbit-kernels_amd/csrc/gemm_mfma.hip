@@ -579,12 +579,15 @@ hipError_t dispatch_rows(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, fl
 }  // namespace
 
 // One tile per workgroup beats row groups, from an MI355X sweep (graph-timed, cold weights, M = 2..64 on the
-// Qwen2.5-1.5B/3B/7B projections; bench.py --sweep tiles), on the attention-sized layers: up to 288 tiles (N <= 4608)
-// and K short enough that every wave's own activation loads (4 KB per 1 KB of weights per 16 rows of M) stay cheap,
-// KC * MT <= 64 (K <= 3584 up to M = 32, K <= 2048 up to M = 64): 1.1-2.4x (2048 x 2560, M = 16: 13.3 -> 5.6 us;
-// M = 48 and 64, where row groups split K over workgroups: 18.5 -> 10.7 and 20.1 -> 13.1 us). Long K (8960 and up,
-// or 3584 from 33 rows) and wide N keep row groups, which share the activations through LDS.
-bool tiles_win(int MT, int ntiles, int KC) { return MT <= 4 && ntiles <= 288 && KC * MT <= 64; }
+// Qwen2.5-1.5B/3B/7B projections), on the attention-sized layers: up to 256 tiles (one round of workgroups), K up to
+// 4096 (KC <= 32) and KC * M <= 256 (384 for K <= 1536), i.e. while every wave's own activation loads (4 KB per 1 KB
+// of weights per 16 rows of M) stay cheap: 2048 x 2560 at M = 16 5.7 us against 6.3 for the best row-group plan,
+// 1536 x 2048 at M = 32 6.6 against 6.9, 3584 x 3584 at M = 8 6.6 against 7.9; 2048 x 2048 at M = 24 7.4 against
+// 7.0 with row groups. Past that, row groups with K split over workgroups (since the split partials are handed over
+// without an L2 write-back) win: 2048 x 2048 at M = 32 7.0 against 8.0, at M = 48 7.9 against 10.2; 3584 x 3584 at
+// M = 16 8.0 against 8.4; 3584 x 4608 (288 tiles) at M = 16 8.2 against 12.5. Long K (8960 and up) keeps row groups
+// at every M (11008 x 2048, M = 2: 9.9 against 12.9).
+bool tiles_win(int M, int ntiles, int KC) { return ntiles <= 256 && KC <= 32 && KC * M <= (KC <= 12 ? 384 : 256); }
 
 // deepest ring the one-tile kernel holds without spilling at 8 waves (hipcc -O3, gfx950: 112 / 186 / 204 registers at
 // MT = 1 / 2 / 3 with 4 / 4 / 3 slots; MT = 4 spills at 3 slots)
@@ -618,10 +621,11 @@ int balanced_tile_waves(int ntiles, int MT) {
 }
 
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
-// tile per wave; K split across workgroups while the row groups times the split stay within ~320 workgroups (narrow
-// N), only for layers with fewer than 128 row groups (each split workgroup pays an agent-scope release to hand over
-// its partial sums, which a layer already spread over half the CUs does not earn back: 1536 x 8960, 140 row groups,
-// split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, gains from 4 ways); K-groups per workgroup until
+// tile per wave; K split across workgroups while the row groups times the split stay within 256 workgroups (narrow
+// N), every split keeps at least 4 chunks and K has at least 16 (1536 x 2048 at M = 48: 8.4 us unsplit against 8.9
+// split 2 ways), only for layers with fewer than 128 row groups (1536 x 8960, 140 row
+// groups, split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, 4 ways; 2048 x 2048 at M = 32 7.0 us with
+// 4 ways against 8.4 with 8; 3584 x 4608, 72 row groups, 9.6 with 2 against 10.8 with 4); K-groups per workgroup until
 // about kGemmTargetWaves waves run (at most 2 K-groups for 17..32 rows; up to 16 rows 4, also where the row groups
 // alone reach that many waves: 3584 x 16384, 256 row groups, M = 16, 10.3 -> 9.6 us against 2); from 33 rows K-groups
 // double only while the waves stay within kGemmMaxWavesWide (3B gate/up at M = 64 12.3 us with 2 K-groups against
@@ -633,8 +637,8 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   const GemvOverride o = gemv_override();
   const int ntiles = (N + 15) / 16, KC = K / 128;
   p.MT = (M + 15) / 16;
-  if (p.MT <= 4 && row_tiles == 0 && (o.gemm_kernel == 2 || (o.gemm_kernel == 0 && tiles_win(p.MT, ntiles, KC)))) {
-    int waves = ntiles <= 256 && KC >= 24 ? 8 : 4;            // same sweep
+  if (p.MT <= 4 && row_tiles == 0 && (o.gemm_kernel == 2 || (o.gemm_kernel == 0 && tiles_win(M, ntiles, KC)))) {
+    int waves = KC >= 16 ? 8 : 4;                             // same sweep (2048 x 2048, M = 2: 4.35 us against 4.84)
     if (o.waves > 0) waves = o.waves;
     waves = std::min(waves, 8);
     while (waves > 1 && waves > KC) waves /= 2;
@@ -653,7 +657,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   if (o.splits > 0) {
     S = o.splits;
   } else if (part_bytes > 0) {
-    while (S < kMaxSplits && groups < 128 && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 2 * S) S *= 2;
+    while (S < kMaxSplits && groups < 128 && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 8 * S && KC >= 16) S *= 2;
   }
   S = std::min(S, std::max(1, KC));
   while (S > 1 && (size_t)S * M * N * sizeof(float) > part_bytes) --S;
@@ -665,11 +669,16 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     ks = KW == 3 && p.MT == 1 ? 4 : 2;                      // same sweep: 3584 x 18944, M = 48, 20.6 -> 16.8 us), 4
   } else if (p.MT == 1 && S == 1) {                         // for 3 tile-waves at 16 rows (2048 x 11008: 7.19 -> 6.46)
     while (ks < 4 && 2 * ks <= KC) ks *= 2;
-  } else if (p.MT <= 2) {                                  // up to 4 K-groups for 16 rows, 2 for 32 (same sweep:
-    const int kmax = p.MT == 1 ? 4 : 2;                     // 2048 x 11008 at M = 32, 8.6 -> 8.2 us with 2)
-    while (ks < kmax && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
-  } else {                                                  // from 33 rows: fewer, longer K-groups (see above)
-    while (ks < 4 && (long)groups * S * KW * 2 * ks <= kGemmMaxWavesWide && 2 * ks * S <= KC) ks *= 2;
+  } else if (p.MT <= 2) {
+    // a K split up to 16 rows, or 17-32 rows: 2 K-groups (2048 x 11008 at M = 32 8.2 us against 8.6 with 1; split
+    // layers at M = 16: 8960 x 1536 9.7 against 10.1 with 4)
+    while (ks < 2 && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
+  } else {
+    // from 33 rows: fewer, longer K-groups (see above), and on an unsplit layer at least 4 chunks each (1536 x 2048
+    // at M = 48: 7.97 us with 2 against 8.35 with 4); but up to 4 on layers split 4 or more ways (11008 x 2048 at
+    // M = 48 13.3 us against 15.2 with 2; 2048 x 2560 8.1 against 9.1; 3584 x 3584 10.4 against 11.0)
+    const long cap = S >= 4 ? 2L * kGemmMaxWavesWide : (long)kGemmMaxWavesWide;
+    while (ks < 4 && (long)groups * S * KW * 2 * ks <= cap && 2 * ks * S <= KC && (S > 1 || 8 * ks <= KC)) ks *= 2;
   }
   while (ks > 1 && ks * S > KC) ks /= 2;
   p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);

@@ -138,7 +138,7 @@ constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many byte
 // MFMA GEMM launch shape: K splits across workgroups up to kGemmMaxGroups workgroups (at most kMaxSplits ways), then
 // K-groups inside a workgroup up to kGemmTargetWaves waves. A workspace starts with kCounterBytes of arrival
 // counters (zero before first use, left zero by every launch), followed by the fp32 partial sums [splits][M][N].
-constexpr int kGemmMaxGroups = 320;
+constexpr int kGemmMaxGroups = 256;
 constexpr int kGemmTargetWaves = 1792;
 constexpr int kGemmMaxWavesWide = 2048;
 // prefill GEMM: K is split while the work items fill fewer than two rounds of this many workgroups

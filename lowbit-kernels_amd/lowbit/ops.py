@@ -163,13 +163,13 @@ AUTO_GEMV_NARROW_ROWS, AUTO_GEMV_NARROW_N, AUTO_GEMV_MAX_K = 3, 8192, 16384
 # Beyond the MFMA kernel's rows (prefill), a weight on the mma layout goes to the int4-direct prefill GEMM (prefill())
 # when K >= AUTO_PREFILL_MIN_K, when M <= AUTO_PREFILL_ROWS, or when M <= AUTO_PREFILL_NARROW_ROWS on a small layer
 # (N and K <= AUTO_PREFILL_NARROW); everything else dequantizes (4.4-4.8 TB/s) and calls BLAS. From the MI355X sweep at
-# M = 128, 256, 512, 2048 on the Qwen2.5-3B / 7B projections (int4 vs dequantize + hipBLASLt, us): the attention-sized
-# 3B layers up to 512 rows (q|k|v 14.3 vs 21.4 at M = 128, 18.4 vs 25.0 at 512; o 14.3 vs 21.9 at 512), every layer up
-# to 256 rows (3B merged gate|up 27.3 vs 46.4 at 128, 39.7 vs 56.7 at 256; 3B down 32.3 vs 37.4 at 128, 47.0 vs 47.4
-# at 256) and the long-K 7B down at every M (60 vs 109 at 128, 130 vs 202 at 512); dequantize + hipBLASLt keeps the
-# wide and long layers from 512 rows (3B gate|up at 512: 77 vs 89, 3B down 58 vs 67) and the small ones at 2048.
-AUTO_PREFILL_MIN_K, AUTO_PREFILL_ROWS = 16384, 256
-AUTO_PREFILL_NARROW, AUTO_PREFILL_NARROW_ROWS = 4096, 512
+# M = 128, 256, 512, 2048 on the Qwen2.5-3B / 7B projections (int4 vs dequantize + hipBLASLt, us): every layer up to
+# 512 rows (3B merged gate|up 26.3 vs 45.9 at 128, 72.6 vs 75.9 at 512; 3B down 26.0 vs 38.3 at 128, 49.0 vs 58.4 at
+# 512; 7B gate|up 97.8 vs 100.8 at 512), the attention-sized 3B layers up to 2048 rows (o 29.2 vs 31.7, q|k|v 36.9 vs
+# 36.6 at 2048) and the long-K 7B down at every M (47 vs 109 at 128, 119 vs 203 at 512, 345 vs 395 at 2048);
+# dequantize + hipBLASLt keeps the wide and long layers at 2048 rows (3B gate|up 190 vs 261, 3B down 107 vs 134).
+AUTO_PREFILL_MIN_K, AUTO_PREFILL_ROWS = 16384, 512
+AUTO_PREFILL_NARROW, AUTO_PREFILL_NARROW_ROWS = 4096, 2048
 
 
 def gemm_chunked(x, wq, chunk=64):
