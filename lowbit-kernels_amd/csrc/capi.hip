@@ -438,7 +438,9 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
   if (!(g == 1 || g == 2 || g == 4 || g == 6 || g == 7 || g == 8))
     return fail(LOWBIT_ERR_SHAPE, "attention takes 1, 2, 4, 6, 7 or 8 query heads per KV head");
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return fail(LOWBIT_ERR_ALIGN, "attention needs 16-byte aligned q and caches");
-  if (workspace && !aligned16(workspace)) return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned");
+  if (workspace && (!aligned16(workspace) || workspace_bytes < kAttnCounterBytes))
+    return fail(LOWBIT_ERR_ARG, "the attention workspace must be 16-byte aligned and hold at least %zu bytes",
+                kAttnCounterBytes);
   if (int rc = check_device()) return rc;
   return hip_status(attention_launch(static_cast<const f16*>(q), static_cast<const f16*>(k_cache),
                                      static_cast<const f16*>(v_cache), positions, static_cast<f16*>(out), (int)M,

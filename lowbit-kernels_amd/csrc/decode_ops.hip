@@ -95,18 +95,47 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
 // probabilities never leave the lane that multiplies them into V. Waves take blocks of KB keys; the row groups and
 // the waves are merged at the end (lane shuffles, then LDS).
 // When (token, group) blocks alone cannot fill the chip (a decode step), the keys are also split into P partitions
-// of CH keys (grid.y): each block writes its partial (max, sum, unnormalized output) to the workspace and
-// attention_combine, launched next on the stream, merges the P partials in partition order. The kernel boundary makes
-// the partials visible across XCDs; an in-kernel last-arrival merge would need an agent-scope release per block
-// (an L2 write-back, serialized per XCD), which measured slower than the second launch.
+// of CH keys (grid.y): each block writes its partial (max, sum, unnormalized output) to the workspace with
+// agent-coherent stores (store_partial) and counts its arrival; the last of the P blocks of a (token, group) merges
+// the P partials in partition order (merge_partitions) and writes the output. (With a release per block, an L2
+// write-back, this merge measured slower than a second launch; the coherent stores need none.)
+// Output dim d of one (block, head) from the P <= kAttnMaxParts partials [max, sum, o[128]] at float index `first`,
+// `stride` floats apart: max over partitions, then the rescaled sums in partition order (partitions that saw no key
+// hold max = -inf and are skipped; partition 0 always holds key 0). The loops run to the compile-time bound, so all
+// the loads are requested before the first is used.
+__device__ __forceinline__ float merge_partitions(__amdgpu_buffer_rsrc_t pr, int first, int stride, int P, int d) {
+  float pm[kAttnMaxParts], ps[kAttnMaxParts], po[kAttnMaxParts];
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) {
+    const int at = 4 * (first + p * stride);
+    const bool live = p < P;
+    pm[p] = live ? load_partial(pr, at) : -INFINITY;
+    ps[p] = live ? load_partial(pr, at + 4) : 0.f;
+    po[p] = live ? load_partial(pr, at + 4 * (2 + d)) : 0.f;
+  }
+  float gm = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) gm = fmaxf(gm, pm[p]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int p = 0; p < kAttnMaxParts; ++p) {
+    if (pm[p] == -INFINITY) continue;
+    const float f = expf(pm[p] - gm);
+    num = fmaf(f, po[p], num);
+    den = fmaf(f, ps[p], den);
+  }
+  return num / den;
+}
+
 template <int G, int KB>
 __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k_cache, const f16* __restrict__ v_cache,
     const int64_t* __restrict__ pos, f16* __restrict__ out, int Hq, int Hkv, int L, float scale, int CH,
-    float* __restrict__ part) {
+    uint32_t* __restrict__ ctr, float* __restrict__ part) {
   constexpr int NI = KB / 4;                                 // 16-byte loads per lane and step, per K and per V
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  args_in_sgprs(q, k_cache, v_cache, pos, out, Hq, Hkv, L, CH, part, (int)blockDim.x);
+  __shared__ int s_last;
+  args_in_sgprs(q, k_cache, v_cache, pos, out, Hq, Hkv, L, CH, ctr, part, (int)blockDim.x);
   const int groups = Hq / G, P = gridDim.y, pid = blockIdx.y;
   const int m = blockIdx.x / groups, h0 = (blockIdx.x % groups) * G, hk = h0 / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
@@ -193,7 +222,8 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
   }
   __syncthreads();
   // partial of this block: [G][2 + D] floats (max, sum, then the unnormalized output), per (token, group, partition)
-  float* mine = part + (((size_t)blockIdx.x * P + pid) * G) * (2 + kHeadDim);
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)(gridDim.x * P * G * (2 + kHeadDim) * 4));
+  const int mine = (blockIdx.x * P + pid) * G * (2 + kHeadDim);
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
     const int g = idx / kHeadDim, d = idx % kHeadDim;
     float gm = -INFINITY;
@@ -209,46 +239,42 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
     if (P == 1) {
       out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
     } else {
-      mine[g * (2 + kHeadDim) + 2 + d] = num;
+      const int at = 4 * (mine + g * (2 + kHeadDim));
+      store_partial(pr, at + 4 * (2 + d), num);
       if (d == 0) {
-        mine[g * (2 + kHeadDim)] = gm;
-        mine[g * (2 + kHeadDim) + 1] = den;
+        store_partial(pr, at, gm);
+        store_partial(pr, at + 4, den);
       }
     }
   }
+  if (P == 1) return;
+  // count this block's arrival once its partials are acknowledged; the last of the P merges them
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(P - 1);
+  __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (!s_last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
+    const int g = idx / kHeadDim, d = idx % kHeadDim;
+    out[((size_t)m * Hq + h0 + g) * kHeadDim + d] =
+        (f16)merge_partitions(pr, blockIdx.x * P * G * (2 + kHeadDim) + g * (2 + kHeadDim), G * (2 + kHeadDim), P, d);
+  }
 }
 
-// out[m][h][d] from the P <= kAttnMaxParts partials of attention_kernel: max over partitions, then the rescaled sums,
-// in partition order (partitions that saw no key hold max = -inf and are skipped; partition 0 always holds key 0).
-// The loops run to the compile-time bound, so all of a thread's loads are requested before the first is used.
+// out[m][h][d] from the P <= kAttnMaxParts partials of attention_mfma (merge_partitions), launched after it
 __global__ __launch_bounds__(256) void attention_combine(const float* __restrict__ part, f16* __restrict__ out,
                                                          int blocks, int G, int P, int Hq) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= blocks * G * kHeadDim) return;
   const int b = idx / (G * kHeadDim), g = (idx / kHeadDim) % G, d = idx % kHeadDim;
   const int groups = Hq / G, m = b / groups, h = (b % groups) * G + g;
-  const float* all = part + (size_t)b * P * G * (2 + kHeadDim) + (size_t)g * (2 + kHeadDim);
-  const size_t stride = (size_t)G * (2 + kHeadDim);
-  float pm[kAttnMaxParts], ps[kAttnMaxParts], po[kAttnMaxParts];
-#pragma unroll
-  for (int p = 0; p < kAttnMaxParts; ++p) {
-    const bool live = p < P;
-    pm[p] = live ? all[p * stride] : -INFINITY;
-    ps[p] = live ? all[p * stride + 1] : 0.f;
-    po[p] = live ? all[p * stride + 2 + d] : 0.f;
-  }
-  float gm = -INFINITY;
-#pragma unroll
-  for (int p = 0; p < kAttnMaxParts; ++p) gm = fmaxf(gm, pm[p]);
-  float num = 0.f, den = 0.f;
-#pragma unroll
-  for (int p = 0; p < kAttnMaxParts; ++p) {
-    if (pm[p] == -INFINITY) continue;
-    const float f = expf(pm[p] - gm);
-    num = fmaf(f, po[p], num);
-    den = fmaf(f, ps[p], den);
-  }
-  out[((size_t)m * Hq + h) * kHeadDim + d] = (f16)(num / den);
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)(blocks * P * G * (2 + kHeadDim) * 4));
+  out[((size_t)m * Hq + h) * kHeadDim + d] =
+      (f16)merge_partitions(pr, b * P * G * (2 + kHeadDim) + g * (2 + kHeadDim), G * (2 + kHeadDim), P, d);
 }
 
 // Causal GQA attention on MFMA for multi-token steps and prompts (same contract as attention_kernel): one wave per
@@ -495,11 +521,12 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   // key partitions: when the (token, group) blocks cannot fill the chip, split the keys so that about
   // kAttnTargetBlocks blocks run, each with at least kAttnMinKeys keys, within the workspace and its counters
   int P = 1;
-  if (ws && blocks < kAttnTargetBlocks && max_keys >= kAttnMinSplitKeys) {
+  if (ws && ws_bytes > kAttnCounterBytes && blocks < kAttnTargetBlocks && blocks <= (long)(kAttnCounterBytes / 4) &&
+      max_keys >= kAttnMinSplitKeys) {
     P = (int)std::min<long>({(kAttnTargetBlocks + blocks - 1) / blocks, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
                              (long)kAttnMaxParts});
     const size_t per = (size_t)blocks * G * (2 + kHeadDim) * sizeof(float);
-    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, ws_bytes / per));
+    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, (ws_bytes - kAttnCounterBytes) / per));
   }
   const int CH = ((max_keys + P - 1) / P + KB - 1) / KB * KB;   // keys per partition, whole steps
   P = (max_keys + CH - 1) / CH;
@@ -509,13 +536,10 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   // costs more than the keys they share out (measured: 3B prompt of 512 tokens 58 -> 48 us, 7B 99 -> 70 us)
   if (blocks * P >= kAttnManyBlocks && waves > 4) waves = 4;
   const size_t lds = (size_t)waves * G * 2 * 4 + (size_t)waves * G * kHeadDim * 4;
-  float* part = static_cast<float*>(ws);
-  hipError_t e = launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos,
-                        out, Hq, Hkv, L, scale, CH, part);
-  if (e != hipSuccess || P == 1) return e;
-  const long threads = blocks * G * kHeadDim;
-  return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, (int)blocks,
-                G, P, Hq);
+  uint32_t* ctr = static_cast<uint32_t*>(ws);
+  float* part = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kAttnCounterBytes) : nullptr;
+  return launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos, out, Hq,
+                Hkv, L, scale, CH, ctr, part);
 }
 // multi-token steps and prompts on MFMA: one wave per (KV head, 16 query rows, key partition); partitions while the
 // waves number fewer than kAttnMfmaTargetWaves, at most one per kAttnMinKeys of max_keys, within the workspace (each
@@ -526,13 +550,14 @@ hipError_t launch_attention_mfma(const f16* q, const f16* k, const f16* v, const
   const int G = Hq / Hkv;
   const long waves = (long)((M * G + 15) / 16) * Hkv;
   int P = 1;
-  if (ws && waves < kAttnMfmaTargetWaves && max_keys >= 2 * kAttnMinKeys) {
+  if (ws && ws_bytes > kAttnCounterBytes && waves < kAttnMfmaTargetWaves && max_keys >= 2 * kAttnMinKeys) {
     P = (int)std::min<long>({(kAttnMfmaTargetWaves + waves - 1) / waves, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
                              (long)kAttnMaxParts});
     const size_t per = (size_t)M * Hkv * G * (2 + kHeadDim) * sizeof(float);
-    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, ws_bytes / per));
+    P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, (ws_bytes - kAttnCounterBytes) / per));
   }
-  float* part = static_cast<float*>(ws);
+  // the partials after the decode kernel's arrival counters, which this kernel leaves untouched
+  float* part = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kAttnCounterBytes) : nullptr;
   hipError_t e = launch(attention_mfma, dim3((unsigned)waves, P), dim3(64), 0, st, q, k, v, pos, out, M, Hq, Hkv, L,
                         scale, part);
   if (e != hipSuccess || P == 1) return e;

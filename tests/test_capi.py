@@ -87,6 +87,8 @@ def _msg(rc):
     (lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, FAKE, 0, None), 3, "M must be positive"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, ctypes.c_void_p(4098), 4, None), 4, "4-byte aligned"),
+    (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,
+                                  None), 1, "at least 4096 bytes"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 5, 16, 128, None), 5, "1..4 rows"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 1, 16, 12, None), 3, "K % 8"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 4, 16, 16384, None), 3, "K % 8"),
