@@ -27,25 +27,39 @@ __device__ __forceinline__ float block_sum(float v, float* red) {    // all thre
 }  // namespace
 
 // out[m] = w * fp16(x[m] / sqrt(mean(x[m]^2) + eps)), one block per row (Qwen2RMSNorm: the normalisation in fp32,
-// rounded to fp16, then the fp16 product with the weight)
+// rounded to fp16, then the fp16 product with the weight). The first kNormPieces 16-byte pieces of x and w per thread
+// (H <= 8192 at 256 threads) are loaded once, before the block reduction, and kept in registers for the output: one
+// memory round trip instead of two; longer rows reload the rest.
+constexpr int kNormPieces = 4;
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
                                                       f16* __restrict__ out, int H, float eps) {
   __shared__ float red[4];
   const size_t row = (size_t)blockIdx.x * H;
+  const int step = blockDim.x * 8;
+  u32x4 xv[kNormPieces], wv[kNormPieces];
+#pragma unroll
+  for (int c = 0; c < kNormPieces; ++c) {
+    const int i = threadIdx.x * 8 + c * step;
+    if (i < H) {
+      xv[c] = *reinterpret_cast<const u32x4*>(x + row + i);
+      wv[c] = *reinterpret_cast<const u32x4*>(w + i);
+    }
+  }
   float ss = 0.f;
-  for (int i = threadIdx.x * 8; i < H; i += blockDim.x * 8) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(x + row + i);
+  auto add_squares = [&](const u32x4& v) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f16x2 p = as_f16x2(v[j]);
       ss = fmaf((float)p[0], (float)p[0], ss);
       ss = fmaf((float)p[1], (float)p[1], ss);
     }
-  }
+  };
+#pragma unroll
+  for (int c = 0; c < kNormPieces; ++c)
+    if (threadIdx.x * 8 + c * step < H) add_squares(xv[c]);
+  for (int i = threadIdx.x * 8 + kNormPieces * step; i < H; i += step) add_squares(*reinterpret_cast<const u32x4*>(x + row + i));
   const float r = rsqrtf(block_sum(ss, red) / (float)H + eps);
-  for (int i = threadIdx.x * 8; i < H; i += blockDim.x * 8) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(x + row + i);
-    const u32x4 g = *reinterpret_cast<const u32x4*>(w + i);
+  auto store_norm = [&](int i, const u32x4& v, const u32x4& g) {
     u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -54,7 +68,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16* __restrict__ x,
       o[j] = as_u32(f16x2{(f16)((float)wj[0] * (float)n[0]), (f16)((float)wj[1] * (float)n[1])});
     }
     *reinterpret_cast<u32x4*>(out + row + i) = o;
+  };
+#pragma unroll
+  for (int c = 0; c < kNormPieces; ++c) {
+    const int i = threadIdx.x * 8 + c * step;
+    if (i < H) store_norm(i, xv[c], wv[c]);
   }
+  for (int i = threadIdx.x * 8 + kNormPieces * step; i < H; i += step)
+    store_norm(i, *reinterpret_cast<const u32x4*>(x + row + i), *reinterpret_cast<const u32x4*>(w + i));
 }
 
 // qkv [M][(Hq + 2 Hkv) D] (the fused projection's output, bias included) -> q_out [M][Hq][D] with RoPE; k (with
