@@ -252,8 +252,10 @@ def test_qkv_rope_rows_equal_projection_then_rope(cuda, hq, hkv, k, m):
                                                 (16, 2, 768, list(range(512, 528))), (16, 2, 600, list(range(100, 400))),
                                                 (12, 2, 300, list(range(0, 300, 37)))])
 def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
-    """Decode steps (a few tokens: one block per (token, head group), key partitions merged by a second launch) and
-    multi-token steps and prompts (from 32 query rows per KV head: the MFMA kernel, with and without partitions)."""
+    """Decode steps (a few tokens: one block per (token, head group), key partitions merged by the last block of
+    each (token, head group) to finish, through arrival counters at the workspace's head) and multi-token steps and
+    prompts (from 32 query rows per KV head: the MFMA kernel, with and without partitions, merged by a second
+    launch). Repeated calls give the same bits and leave the counters at zero."""
     g = torch.Generator(device="cuda").manual_seed(hq + L)
     m = len(positions)
     q = torch.randn(m, hq, 128, generator=g, device="cuda").half()
@@ -277,6 +279,10 @@ def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
         again = torch.empty_like(out)
         ops.ext().attention(q, k_cache, v_cache, pos, again, hq, hkv, max_keys, scale, split=split)
         assert torch.equal(out, again), (split, max_keys)
+    st = _native._stream(q.device)
+    ws = _native.workspace(q.device, st, _native.ATTENTION_WORKSPACE_BYTES)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(ws[:4096])) == 0
 
 
 @pytest.fixture(scope="module")
