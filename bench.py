@@ -326,9 +326,16 @@ def provenance(torch, ops):
                                 timeout=10).stdout.strip() or None
     except (OSError, subprocess.SubprocessError):
         commit = None
+    built_from = None                                       # the commit the library was built from (build.py)
+    info = pkg / "lowbit" / "build_info.json"
+    if info.exists():
+        try:
+            built_from = json.loads(info.read_text())
+        except ValueError:
+            built_from = None
     return {"gpu": props.name, "gcn_arch": getattr(props, "gcnArchName", None), "cus": props.multi_processor_count,
             "hbm_gib": round(props.total_memory / 2 ** 30, 1), "torch": torch.__version__,
-            "hip": getattr(torch.version, "hip", None), "git_commit": commit,
+            "hip": getattr(torch.version, "hip", None), "git_commit": commit, "library_built_from": built_from,
             "sources_sha256": _sha256_files([q for q in sources if q.is_file()]),
             "library_sha256": _sha256_files([lib]) if lib.exists() else None,
             "library": ops._native.lib().lowbit_version().decode(),

@@ -103,7 +103,26 @@ def build(jobs=None, asm=False, verbose=False, outdir=BUILD, out=OUT, extra=()):
     os.replace(tmp, out)
     if out == OUT:
         build_format()
+        write_build_info()
     return out
+
+
+BUILD_INFO = PKG / "lowbit" / "build_info.json"
+
+
+def write_build_info(path=BUILD_INFO):
+    """The git commit the library was built from (and whether the tree had uncommitted changes), beside the library,
+    for provenance records made where the tree travels without its git history."""
+    import json
+    def git(*args):
+        try:
+            p = subprocess.run(["git", "-C", str(ROOT), *args], capture_output=True, text=True, timeout=10)
+            return p.stdout.strip() if p.returncode == 0 else None
+        except (OSError, subprocess.SubprocessError):
+            return None
+    status = git("status", "--porcelain", "--untracked-files=no")
+    path.write_text(json.dumps({"git_commit": git("rev-parse", "HEAD"),
+                                "uncommitted_changes": None if status is None else bool(status)}) + "\n")
 
 
 def sanitizer_check(jobs=None):
