@@ -147,3 +147,27 @@ def test_quant_runs_without_the_kernel_library(tmp_path):
                PYTHONPATH=os.pathsep.join([str(root / "lowbit-kernels_amd"), str(root)]))
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and out.stdout.strip() == "ok", out.stderr[-2000:]
+
+
+def test_build_info_names_the_commit_the_library_was_built_from(tmp_path):
+    """build.py records the git commit (and whether the tree had uncommitted changes) beside the library, for the
+    bench's provenance on machines where the tree travels without its history."""
+    import json
+    import subprocess
+    import sys
+    pkg = pathlib.Path(__file__).resolve().parent.parent / "lowbit-kernels_amd"
+    sys.path.insert(0, str(pkg))
+    try:
+        import build as lowbit_build
+    finally:
+        sys.path.remove(str(pkg))
+    out = tmp_path / "build_info.json"
+    lowbit_build.write_build_info(out)
+    info = json.loads(out.read_text())
+    assert set(info) == {"git_commit", "uncommitted_changes"}
+    head = subprocess.run(["git", "-C", str(pkg.parent), "rev-parse", "HEAD"], capture_output=True, text=True)
+    if head.returncode == 0:
+        assert info["git_commit"] == head.stdout.strip()
+        assert isinstance(info["uncommitted_changes"], bool)
+    else:                                                   # a copy of the tree without its git history
+        assert info["git_commit"] is None
