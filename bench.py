@@ -86,8 +86,10 @@ def parse():
                          "give the spread")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "tiles", "tilewaves", "splits"], default=None,
+    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "ldsring", "tiles", "tilewaves", "splits"],
+                    default=None,
                     help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
+                         "ldsring: the M=1 GEMV's weight ring in registers vs in LDS; "
                          "tiles: the MFMA GEMM's row groups vs one tile per workgroup, M=2..32; "
                          "tilewaves: the row groups' tile-waves and K-groups on layers of 560 to 2368 tiles; "
                          "splits: the row groups' K split x K-groups on the decode projections, M=16..64")
@@ -163,12 +165,15 @@ def cpu_model():
     return None
 
 
-def cpu_breakdown(k=896, n=4864, rounds=5):
-    """BASELINE configs[0] on the host: M=1, K=896, N=4864, weights N(0, 0.02), x N(0, 1) fp16, absmax g128. Median
-    milliseconds per call (after one warm-up) of (i) the reference's torch dequantize to fp16 + torch linear, (ii)
-    torch linear on the pre-dequantized fp16 weight, (iii) quantize (one-off; the reference's numpy quantizer, which
-    is single-threaded either way), with torch on all its threads and on one. The fp64 error of the result is
-    reported beside."""
+def cpu_breakdown(k=896, n=4864, rounds=25):
+    """BASELINE configs[0] on the host: M=1, K=896, N=4864, weights N(0, 0.02), x N(0, 1) fp16, absmax g128. Per call
+    (milliseconds, min and median of `rounds` after 3 warm-up calls each) of (i) the reference's torch dequantize to
+    fp16 + torch linear, (ii) the dequantize alone, (iii) torch linear on the pre-dequantized fp16 weight, (iv)
+    quantize (one-off; the reference's numpy quantizer, single-threaded either way), with torch on all its threads
+    and on one. The thread count is set before the warm-up, and the cells are timed round-robin (one call of each
+    per round), so a slow stretch of the host hits every cell alike. (i) does (ii)'s work and more, so its min must
+    not be below (ii)'s: a run where it is is timed again (once), and `ordering_ok` reports the check. The fp64
+    error of the result is reported beside."""
     import numpy as np
     import torch
     from oracle import quant_ref as R
@@ -177,27 +182,37 @@ def cpu_breakdown(k=896, n=4864, rounds=5):
     x = torch.from_numpy(rng.standard_normal((1, k)).astype(np.float16))
     packed, scales = R.quantize_w4(w, GROUP)
     w16 = torch.from_numpy(R.dequantize_w4_f16(packed, scales, GROUP))
+    cells = {"dequant_linear_ms": lambda: R.cpu_torch_linear(x, packed, scales, GROUP),
+             "dequant_only_ms": lambda: R.dequantize_w4_torch(packed, scales, GROUP),
+             "linear_only_ms": lambda: torch.nn.functional.linear(x, w16),
+             "quantize_ms": lambda: R.quantize_w4(w, GROUP)}
 
-    def med(fn):
-        fn()
-        ts = []
+    def timed():
+        for fn in cells.values():
+            for _ in range(3):
+                fn()
+        ts = {name: [] for name in cells}
         for _ in range(rounds):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return round(sorted(ts)[len(ts) // 2] * 1e3, 3)
+            for name, fn in cells.items():
+                t0 = time.perf_counter()
+                fn()
+                ts[name].append(time.perf_counter() - t0)
+        return {name: {"min": round(min(v) * 1e3, 4), "median": round(sorted(v)[len(v) // 2] * 1e3, 4)}
+                for name, v in ts.items()}
 
     full = torch.get_num_threads()
     out = {"shape": {"M": 1, "K": k, "N": n, "group": GROUP}, "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
-           "torch_threads": full, "unit": "ms per call (median of %d)" % rounds}
+           "torch_threads": full, "unit": f"ms per call, min and median of {rounds} round-robin rounds"}
+    ok = True
     for threads in (full, 1):
         torch.set_num_threads(threads)
-        out[f"threads_{threads}"] = {
-            "dequant_linear_ms": med(lambda: R.cpu_torch_linear(x, packed, scales, GROUP)),
-            "dequant_only_ms": med(lambda: R.dequantize_w4_torch(packed, scales, GROUP)),
-            "linear_only_ms": med(lambda: torch.nn.functional.linear(x, w16)),
-            "quantize_ms": med(lambda: R.quantize_w4(w, GROUP))}
+        cell = timed()
+        if cell["dequant_linear_ms"]["min"] < cell["dequant_only_ms"]["min"]:
+            cell = timed()
+        ok &= cell["dequant_linear_ms"]["min"] >= cell["dequant_only_ms"]["min"]
+        out[f"threads_{threads}"] = cell
     torch.set_num_threads(full)
+    out["ordering_ok"] = bool(ok)
     y = torch.nn.functional.linear(x, w16).numpy()
     out["rel_err_vs_fp64"] = R.rel_err(y, R.gemv_reference(x.double().numpy(), packed, scales, GROUP))
     return out
@@ -616,6 +631,46 @@ def sweep_gemv(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+LDS_RING_SHAPES = [(896, 4864), (1536, 256), (1536, 1536), (1536, 8960), (1536, 17920), (8960, 1536), (2048, 256),
+                   (2048, 2048), (2048, 2560), (2048, 11008), (2048, 22016), (11008, 2048), (3584, 18944),
+                   (18944, 3584)]
+
+
+def sweep_ldsring(a):
+    """M=1 GEMV (v6) per decode shape: graph-timed us per call with the weight ring in registers (automatic plan)
+    against the ring in LDS (lowbit_set_gemv_lds_ring: 4, 8, 12, 16 slots per wave) at the automatic wave count and
+    at every wave count 1..16 (lowbit_set_launch_override, the automatic tile split)."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in LDS_RING_SHAPES:
+        cl = cloned_copies(torch, ops, k, n)
+        x = torch.randn(1, k, device="cuda").half()
+        t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 6), max(400, len(cl))), 2)
+        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+        _native.check(lib.lowbit_set_gemv_lds_ring(-1))
+        r = {"K": k, "N": n, "registers_us": t(), "lds_us": {}}
+        for lr in (4, 8, 12, 16):
+            _native.check(lib.lowbit_set_gemv_lds_ring(lr))
+            for waves in (0, 1, 2, 4, 8, 16):
+                if waves and waves > k // 128:
+                    continue
+                _native.check(lib.lowbit_set_launch_override(waves, 0, 0))
+                r["lds_us"][f"{lr}x{waves}"] = t()
+        _native.check(lib.lowbit_set_launch_override(0, 0, 0))
+        _native.check(lib.lowbit_set_gemv_lds_ring(0))
+        best = min(r["lds_us"], key=r["lds_us"].get)
+        r["best_lds"] = [best, r["lds_us"][best]]
+        rows.append(r)
+        print(json.dumps(r), flush=True)
+        del cl
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
 def sweep_tiles(a):
     """MFMA GEMM (v5) per decode shape and M in 2..64: graph-timed us per call of the row-group kernel (automatic
     shape), of one tile per workgroup with 2, 4 and 8 waves, and of the automatic choice (lowbit_set_gemm_kernel)."""
@@ -1021,6 +1076,8 @@ def main():
         sweep_prefill(a)
     elif a.sweep == "gemv":
         sweep_gemv(a)
+    elif a.sweep == "ldsring":
+        sweep_ldsring(a)
     elif a.sweep == "tiles":
         sweep_tiles(a)
     elif a.sweep == "tilewaves":

@@ -66,6 +66,13 @@ const char* lowbit_version(void);
  * choices). */
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
 
+/* Process-wide choice of where the M = 1 v6 GEMV keeps its weight ring, for tuning sweeps and tests: 0 = automatic;
+ * -1 = in registers (4 slots per wave); 4, 8, 12 or 16 = that many 1 KB slots per wave in LDS, filled by
+ * direct-to-LDS loads (fewer when the workgroup's LDS would not fit a CU). The sums are formed in the same order
+ * either way, so the results are identical bit for bit. Affects later launches only. No counterpart in the
+ * reference. */
+int lowbit_set_gemv_lds_ring(int slots);
+
 /* Process-wide choice of the MFMA GEMM's structure (lowbit_w4_gemm_mfma, lowbit_w4_linear_fused for M >= 2), for
  * tuning sweeps and tests: 0 = automatic; 1 = row groups of 64 or 128 weight rows sharing staged activations, K split
  * across workgroups on narrow layers; 2 = one 16-row tile per workgroup, its waves splitting K (M <= 32 only; larger M
@@ -208,10 +215,13 @@ int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]
- * (at most L); scores scaled by `scale`, softmax and P.V in fp32. max_keys: an upper bound on positions[m] + 1 over
+ * (at most L); scores scaled by `scale`, softmax and P.V in fp32. Cache rows past the largest position of the call
+ * are never read into a result (they may hold anything, NaN included); rows up to it must be finite, since a
+ * multi-token step reads whole 32-key blocks up to the largest position of the rows it groups. max_keys: an upper bound on positions[m] + 1 over
  * the calls that will run (sizes the launch; a captured graph keeps it; keys past it are still attended, by the last
  * key partition). Hq / Hkv in {1, 2, 4, 6, 7, 8}. workspace (optional, 16-byte aligned, at least 4096 bytes, the
- * first 4096 zero before the first call: arrival counters that every call leaves zero): when there are too few
+ * first 4096 zero before the first call: arrival counters that every call leaves zero; from version 0.2 on -- 0.1
+ * needed no initial contents): when there are too few
  * (token, head group) blocks to fill the GPU and max_keys >= 512, the keys are split into partitions whose fp32
  * partial softmax sums (blocks x partitions x (2 + 128) x 4 bytes after the counters, at most workspace_bytes) the
  * last block of each (token, head group) to finish merges in partition order (steps with at least 32 query rows per

@@ -35,7 +35,7 @@ int check_device() {
 }
 
 std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0}, g_override_gemm{0},
-    g_override_tile_waves{0};
+    g_override_tile_waves{0}, g_override_lds_ring{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -120,6 +120,7 @@ GemvOverride gemv_override() {
   o.splits = g_override_splits.load(std::memory_order_relaxed);
   o.gemm_kernel = g_override_gemm.load(std::memory_order_relaxed);
   o.tile_waves = g_override_tile_waves.load(std::memory_order_relaxed);
+  o.lds_ring = g_override_lds_ring.load(std::memory_order_relaxed);
   return o;
 }
 
@@ -182,7 +183,7 @@ using namespace lowbit;
 
 extern "C" {
 
-const char* lowbit_version(void) { return "lowbit_w4 0.1 gfx950"; }
+const char* lowbit_version(void) { return "lowbit_w4 0.2 gfx950"; }
 
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
   if (!(waves_per_group == 0 || waves_per_group == 1 || waves_per_group == 2 || waves_per_group == 4 ||
@@ -194,6 +195,13 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
   g_override_waves.store(waves_per_group, std::memory_order_relaxed);
   g_override_ring.store(ring, std::memory_order_relaxed);
   g_override_splits.store(k_splits, std::memory_order_relaxed);
+  return ok();
+}
+
+int lowbit_set_gemv_lds_ring(int slots) {
+  if (!(slots == 0 || slots == -1 || slots == 4 || slots == 8 || slots == 12 || slots == 16))
+    return fail(LOWBIT_ERR_TUNING, "slots is 0 (auto), -1 (ring in registers), 4, 8, 12 or 16");
+  g_override_lds_ring.store(slots, std::memory_order_relaxed);
   return ok();
 }
 
@@ -227,7 +235,8 @@ int lowbit_w4_gemm_mfma_noalloc(const void* x, const void* w, const void* s, voi
   constexpr size_t kScratch = LOWBIT_NOALLOC_SCRATCH_BYTES;
   // the planner lowers the K split to what the scratch holds; refuse a plan that would not fit it all the same
   const GemvPlan plan = plan_gemm_mfma((int)M, (int)N, (int)K, row_tiles, kScratch);
-  const int groups = ((int)N + 16 * 4 * plan.R - 1) / (16 * 4 * plan.R);
+  // row groups of plan.KW tile-waves x plan.R tiles (one arrival counter each when K is split)
+  const int ntiles = ((int)N + 15) / 16, groups = (ntiles + plan.KW * plan.R - 1) / (plan.KW * plan.R);
   if (plan.S > 1 && ((size_t)plan.S * M * N * sizeof(float) > kScratch - kCounterBytes ||
                      (size_t)groups * sizeof(uint32_t) > kCounterBytes))
     return fail(LOWBIT_ERR_SHAPE, "w4_gemm_mfma_noalloc: %d-way split partials of M=%lld x N=%lld exceed the %zu-byte scratch",

@@ -172,6 +172,50 @@ __device__ __forceinline__ float load_partial(__amdgpu_buffer_rsrc_t r, int offs
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kAgentCoherent));
 }
 
+// ---- direct-to-LDS loads (gfx950: 16 bytes per lane) ----
+// The LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+// One wave-load straight into LDS: lane l's 16 bytes at buffer offset `voffset` land at LDS byte `lds` + 16 l (M0
+// carries the wave-uniform `lds`). Written as inline asm, so the compiler neither inserts waits for it nor holds LDS
+// accesses back behind it: the caller counts these loads itself (lds_wait_read16, lds_wait_barrier). Vector-memory
+// operations of one wave complete in issue order, so "at most N outstanding" means everything but the newest N has
+// landed; a load of the compiler's issued later only makes such a wait longer, never short. m0 is otherwise unused
+// by the kernels that call this (gfx9 LDS instructions do not read it).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, int voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voffset), "s"(r),
+               "s"(lds)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, int voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"(voffset), "s"(r),
+               "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// Wait until at most N of this wave's vector-memory operations are outstanding, then read 16 bytes at LDS byte
+// `addr`. The read and its own wait sit in the same statement, so the value is complete when the statement ends and
+// no instruction the compiler schedules can use it earlier.
+template <int N>
+__device__ __forceinline__ u32x4 lds_wait_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("s_waitcnt vmcnt(%1)\n\tds_read_b128 %0, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "n"(N), "v"(addr)
+               : "memory");
+  return v;
+}
+// Workgroup barrier once at most N of this wave's vector-memory operations are outstanding and its LDS accesses are
+// done: direct-to-LDS loads older than the newest N are then visible to every wave. No cache write-back or invalidate
+// (the compiler's __syncthreads would also drain every load in flight).
+template <int N>
+__device__ __forceinline__ void lds_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ u32x4 load_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }

@@ -347,11 +347,14 @@ __global__ __launch_bounds__(64) void attention_mfma(const f16* __restrict__ q, 
   f32x4 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // K and V rows are read in whole 32-key blocks, clamped to the wave's last attended key: rows past it may never
+  // have been written (NaN or Inf in an uninitialized cache), and a masked key's weight 0 times NaN is still NaN in
+  // the P V product
   for (int kb = kbeg; kb < kend; kb += 32) {
     u32x4 kf[2][4], vf[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const f16* krow = kh + (size_t)min(kb + kr + 4 * t, L - 1) * kHeadDim + 8 * c;
+      const f16* krow = kh + (size_t)min(kb + kr + 4 * t, wmax) * kHeadDim + 8 * c;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kf[t][ks] = *reinterpret_cast<const u32x4*>(krow + 32 * ks);
     }
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(64) void attention_mfma(const f16* __restrict__ q, 
     for (int u = 0; u < 2; ++u)                               // V rows kb + 4 (lane % 8) + j, dims 8 (lane / 8 + 8 u)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        vf[u][j] = *reinterpret_cast<const u32x4*>(vh + (size_t)min(kb + 4 * (lane & 7) + j, L - 1) * kHeadDim +
+        vf[u][j] = *reinterpret_cast<const u32x4*>(vh + (size_t)min(kb + 4 * (lane & 7) + j, wmax) * kHeadDim +
                                                    8 * ((lane >> 3) + 8 * u));
     f32x4 st[2];
 #pragma unroll

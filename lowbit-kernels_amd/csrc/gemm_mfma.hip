@@ -696,6 +696,8 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   }
   p.waves = KW * ks;
   p.S = std::max(S, 1);
+  // one arrival counter per row group of the final shape (R may have dropped to 1 above)
+  if (p.S > 1 && (ntiles + KW * p.R - 1) / (KW * p.R) > (int)(kCounterBytes / 4)) p.S = 1;
   return p;
 }
 

@@ -52,7 +52,14 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 // CS > 1 (R = 1) splits each 16-row tile over CS workgroups of 16 / CS rows, so layers with few tiles still occupy
 // every CU: a wave-load then covers CS consecutive chunks of the workgroup's rows (lane l: chunk l / (64 / CS)), each
 // piece a contiguous 64 * 16 / CS bytes, and the CS partial sums of a row are added across lanes before the waves'.
-template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1>
+//
+// LR > 0 (M = 1, R = 1, x in LDS): the weight ring lives in LDS instead of registers. Each wave owns LR slots of 1 KB
+// and fills them with direct-to-LDS wave-loads (the same 1 KB pieces); at each step it waits for its oldest slot,
+// reads its 16 bytes back, refills the slot LR wave-loads ahead at once and only then decodes. So LR - 1 wave-loads
+// stay in flight through the decode at no register cost, where a register ring can refill a slot only after its
+// registers are decoded. x, the scales and the norm weights also arrive by direct-to-LDS loads, so the compiler issues
+// no vector-memory load before the main loop and every wait on the ring is counted by hand (see dma16).
+template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1, int LR = 0>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
@@ -60,6 +67,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
                                                                            Epilogue epi,
                                                                            const f16* __restrict__ norm_w, float eps) {
   static_assert(CS == 1 || (R == 1 && (CS == 2 || CS == 4)), "a tile splits over 2 or 4 workgroups, one tile each");
+  static_assert(LR == 0 || (M == 1 && R == 1 && kLdsX), "the LDS ring serves the one-row, one-tile GEMV");
   constexpr int RS = 16 / CS;                               // rows of a tile one workgroup owns
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   constexpr int kScaleLoads = 4;                            // scales per thread requested before the ring
@@ -82,17 +90,19 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   // only zeros and stores nothing). The clamp is computed per lane (v_med3); readfirstlane keeps the scale buffer
   // resource built from it in scalar registers, where a per-lane value would make every scale load a waterfall loop.
   const int n0 = 16 * t0 + RS * sub, nrows = __builtin_amdgcn_readfirstlane(max(0, min(RS * R, N - n0)));
-  // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16
+  // LDS: x [M][K] fp16, its zero-weight sums [M][K/32][2] fp32, the scales [nrows][K/G] fp16 (LR > 0: the layout of
+  // gemv_ring_lds, then the ring)
+  const GemvRingLds RL = gemv_ring_lds(K, KG, RS, nwaves, LR, norm);
   f16* lds_x = reinterpret_cast<f16*>(smem);
-  float* lds_xs = reinterpret_cast<float*>(smem + (kLdsX ? (size_t)M * K * 2 : 0));
-  f16* lds_s = reinterpret_cast<f16*>(smem + (kLdsX ? (size_t)M * K * 2 + (size_t)M * (K / 32) * 8 : 0));
+  float* lds_xs = reinterpret_cast<float*>(smem + (LR ? RL.xs : kLdsX ? (size_t)M * K * 2 : 0));
+  f16* lds_s = reinterpret_cast<f16*>(smem + (LR ? RL.s : kLdsX ? (size_t)M * K * 2 + (size_t)M * (K / 32) * 8 : 0));
 
   // 1. x and scale requests
   const int nb = M * (K / 32), ns = nrows * KG;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(ns * 2));
   u32x4 xst[XB][4], wst[XB][4];
-  if (kLdsX) {
+  if (LR == 0 && kLdsX) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
       const int b = (int)threadIdx.x + u * (int)blockDim.x;
@@ -116,10 +126,12 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   // up to kScaleLoads scales per thread, all in flight before the weights (loads complete in issue order, so a
   // thread's later ones, loaded while staging, would each wait for the whole ring)
   uint16_t sst[kScaleLoads];
+  if constexpr (LR == 0) {
 #pragma unroll
-  for (int u = 0; u < kScaleLoads; ++u) {
-    const int i = (int)threadIdx.x + u * (int)blockDim.x;
-    if (i < ns) sst[u] = buffer_load2_nt(sr, 2 * i);
+    for (int u = 0; u < kScaleLoads; ++u) {
+      const int i = (int)threadIdx.x + u * (int)blockDim.x;
+      if (i < ns) sst[u] = buffer_load2_nt(sr, 2 * i);
+    }
   }
 
   // 2. the weight ring
@@ -135,21 +147,43 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     wstep[i] = live ? CS * rows * 64 : 0;                  // bytes from one wave-load's chunks to the next
     srow[i] = live ? (16 * i + rl) * KG : 0;               // this lane's row in the staged scales
   }
-  u32x4 ring[D][R];
+  u32x4 ring[LR ? 1 : D][R];
+  const uint32_t lds0 = lds_addr(smem), ring0 = lds0 + RL.ring + (uint32_t)wave * (uint32_t)(LR << 10);
+  if constexpr (LR > 0) {
+    // x, the scales and the norm weights in 1 KB wave-loads, round robin over the waves, then this wave's first LR
+    // weight wave-loads; x keeps the default policy (every workgroup reads it), the rest is streamed
+    // A 16-byte load that runs past its range reads zeros as a whole, so the scales' range is rounded up to 16
+    // bytes (the next rows' scales, never read), clipped at the end of the scale tensor, whose size the planner
+    // requires to be a multiple of 16 bytes (N K / G % 8 == 0): every scale of the workgroup arrives, and no load
+    // leaves the tensor.
+    const int nxp = (2 * K + 1023) >> 10, nsp = (2 * ns + 1023) >> 10, ngp = norm ? nxp : 0;
+    const __amdgpu_buffer_rsrc_t srd =
+        make_rsrc(s + (size_t)n0 * KG, (uint32_t)min((2 * ns + 15) & ~15, max(0, 2 * (N - n0) * KG)));
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm_w, norm ? (uint32_t)(K * 2) : 0u);
+    for (int p = wave; p < nxp + nsp + ngp; p += nwaves) {
+      if (p < nxp) dma16(xr, (p << 10) + 16 * lane, lds0 + (p << 10));
+      else if (p < nxp + nsp) dma16_nt(srd, ((p - nxp) << 10) + 16 * lane, lds0 + RL.s + ((p - nxp) << 10));
+      else dma16(gr, ((p - nxp - nsp) << 10) + 16 * lane, lds0 + RL.g + ((p - nxp - nsp) << 10));
+    }
 #pragma unroll
-  for (int d = 0; d < D; ++d)
+    for (int d = 0; d < LR; ++d) dma16_nt(wr[0], woff[0] + (wave + nwaves * d) * wstep[0], ring0 + (d << 10));
+    lds_wait_barrier<LR>();                                 // everything but the ring has landed, in every wave
+  } else {
 #pragma unroll
-    for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (wave + nwaves * d) * wstep[i]);
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (wave + nwaves * d) * wstep[i]);
+  }
 
   // 3. stage x with the decode's own dot2 sequence run on zero weights (every nibble 8), over the lo positions
   //    (k % 8 in 0,1,4,5) and the hi positions (2,3,6,7) of each 32-k block: a block of real weights minus these is
   //    2^-24 sum((u - 8) x) (lo) and 2^-20 sum((u - 8) x) (hi), and exactly 0 where the weights are zero.
   const f16x2 z8lo = as_f16x2(0x00080008u), z8hi = as_f16x2(0x00800080u);
-  auto stage_block = [&](int b, const u32x4 (&v)[4]) {
+  auto stage_block = [&](int b, const u32x4 (&v)[4], bool write_x = true) {
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      reinterpret_cast<u32x4*>(lds_x)[4 * b + j] = v[j];
+      if (write_x) reinterpret_cast<u32x4*>(lds_x)[4 * b + j] = v[j];
       lo = dot2(z8lo, as_f16x2(v[j][0]), lo);
       hi = dot2(z8hi, as_f16x2(v[j][1]), hi);
       lo = dot2(z8lo, as_f16x2(v[j][2]), lo);
@@ -158,6 +192,19 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     lds_xs[2 * b] = lo;
     lds_xs[2 * b + 1] = hi;
   };
+  if (LR > 0 && norm) {                                    // x and the norm weights from LDS into registers
+#pragma unroll
+    for (int u = 0; u < XB; ++u) {
+      const int b = (int)threadIdx.x + u * (int)blockDim.x;
+      if (b < nb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          xst[u][j] = reinterpret_cast<const u32x4*>(lds_x)[4 * b + j];
+          wst[u][j] = reinterpret_cast<const u32x4*>(smem + RL.g)[4 * b + j];
+        }
+      }
+    }
+  }
   if (norm) {                                               // RMSNorm of the (single) row before staging it
     __shared__ float ss_red[16];
     float ss = 0.f;
@@ -177,7 +224,8 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
     ss = wave_sum(ss);
     if (lane == 0) ss_red[wave] = ss;
-    __syncthreads();
+    if constexpr (LR > 0) lds_barrier();                    // (not __syncthreads: it would drain the ring)
+    else __syncthreads();
     float tot = 0.f;
     for (int i = 0; i < nwaves; ++i) tot += ss_red[i];
     const float rn = rsqrtf(tot / (float)K + eps);
@@ -196,7 +244,23 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       }
     }
   }
-  if (kLdsX) {
+  if (LR > 0) {                                            // x is in LDS (normalized in registers when norm)
+    if (norm) {
+#pragma unroll
+      for (int u = 0; u < XB; ++u) {
+        const int b = (int)threadIdx.x + u * (int)blockDim.x;
+        if (b < nb) stage_block(b, xst[u]);
+      }
+    } else {
+      for (int b = (int)threadIdx.x; b < nb; b += blockDim.x) {
+        u32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const u32x4*>(lds_x)[4 * b + j];
+        stage_block(b, v, false);
+      }
+    }
+    lds_barrier();
+  } else if (kLdsX) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
       const int b = (int)threadIdx.x + u * (int)blockDim.x;
@@ -209,14 +273,16 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       stage_block(b, v);
     }
   }
+  if constexpr (LR == 0) {
 #pragma unroll
-  for (int u = 0; u < kScaleLoads; ++u) {
-    const int i = (int)threadIdx.x + u * (int)blockDim.x;
-    if (i < ns) reinterpret_cast<uint16_t*>(lds_s)[i] = sst[u];
+    for (int u = 0; u < kScaleLoads; ++u) {
+      const int i = (int)threadIdx.x + u * (int)blockDim.x;
+      if (i < ns) reinterpret_cast<uint16_t*>(lds_s)[i] = sst[u];
+    }
+    for (int i = (int)threadIdx.x + kScaleLoads * (int)blockDim.x; i < ns; i += blockDim.x)   // > 4 per thread only
+      reinterpret_cast<uint16_t*>(lds_s)[i] = buffer_load2_nt(sr, 2 * i);
+    __syncthreads();
   }
-  for (int i = (int)threadIdx.x + kScaleLoads * (int)blockDim.x; i < ns; i += blockDim.x)   // > 4 per thread only
-    reinterpret_cast<uint16_t*>(lds_s)[i] = buffer_load2_nt(sr, 2 * i);
-  __syncthreads();
 
   float acc[R][M];
 #pragma unroll
@@ -278,19 +344,34 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       }
     }
   };
-  int j0 = 0;
-  for (; j0 + D < nj; j0 += D) {                            // a later group follows: refill behind each consume
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = wave + (j0 + d) * nwaves;
-      consume(ring[d], c);
-#pragma unroll
-      for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (c + D * nwaves) * wstep[i]);
+  if constexpr (LR > 0) {
+    // wave-load j sits in slot j % LR; the LR - 1 after it are in flight. Refills past the last wave-load read zeros
+    // (out of the buffer's range: no memory access) and are drained before the LDS is reused.
+    uint32_t slot = ring0;
+    const uint32_t ring_end = ring0 + (uint32_t)(LR << 10);
+    for (int j = 0; j < nj; ++j) {
+      const u32x4 piece[1] = {lds_wait_read16<LR - 1>(slot + 16 * lane)};
+      const int c = wave + j * nwaves;
+      dma16_nt(wr[0], woff[0] + (c + LR * nwaves) * wstep[0], slot);
+      slot = slot + 1024u == ring_end ? ring0 : slot + 1024u;
+      consume(piece, c);
     }
-  }
+    vm_drain();
+  } else {
+    int j0 = 0;
+    for (; j0 + D < nj; j0 += D) {                          // a later group follows: refill behind each consume
 #pragma unroll
-  for (int d = 0; d < D; ++d)                                // the last group, up to D wave-loads, without refills
-    if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
+      for (int d = 0; d < D; ++d) {
+        const int c = wave + (j0 + d) * nwaves;
+        consume(ring[d], c);
+#pragma unroll
+        for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (c + D * nwaves) * wstep[i]);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)                              // the last group, up to D wave-loads, without refills
+      if (j0 + d < nj) consume(ring[d], wave + (j0 + d) * nwaves);
+  }
 
   // RoPE epilogue (M = 1): rows n (dim d of a head) and n + 8 (dim d + 64) -> bias, RoPE, q_out or the caches. The
   // position, the pair's two bias values and inv_freq[d] are requested together by rope_load (before the cross-wave
@@ -443,6 +524,36 @@ __global__ __launch_bounds__(256) void gemv_rowmajor(const f16* __restrict__ x, 
 
 namespace {
 
+// M = 1, one tile per workgroup, weight ring of LR slots per wave in LDS
+template <int CS, int LR>
+hipError_t launch_lds_ring(const GemvArgs& a, int waves) {
+  const int ntiles = (a.N + 15) / 16;
+  dim3 grid(CS == 1 ? ntiles : ntiles * CS), block(64 * waves);
+  const bool fused = a.epi.mode != kEpiStore || a.norm_w;
+  const size_t bytes = std::max<size_t>(gemv_ring_lds(a.K, a.K / a.G, 16 / CS, waves, LR, a.norm_w).total,
+                                        (size_t)waves * 16 * 4);
+  if (fused) {
+    auto k = gemv_mfma_layout<1, 1, 4, true, true, CS, LR>;
+    if (bytes > 65536)
+      if (hipError_t e = allow_lds(k, bytes)) return e;
+    return launch(k, grid, block, bytes, a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+  }
+  auto k = gemv_mfma_layout<1, 1, 4, true, false, CS, LR>;
+  if (bytes > 65536)
+    if (hipError_t e = allow_lds(k, bytes)) return e;
+  return launch(k, grid, block, bytes, a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi, a.norm_w, a.eps);
+}
+
+template <int CS>
+hipError_t dispatch_lds_ring(const GemvArgs& a, int waves, int LR) {
+  switch (LR) {
+    case 4: return launch_lds_ring<CS, 4>(a, waves);
+    case 8: return launch_lds_ring<CS, 8>(a, waves);
+    case 12: return launch_lds_ring<CS, 12>(a, waves);
+    default: return launch_lds_ring<CS, 16>(a, waves);
+  }
+}
+
 template <int M, int R, int D, int CS = 1>
 hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
@@ -542,6 +653,13 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_
   if (o.waves > 0) waves = o.waves;
   p.D = ((o.ring == 4 || o.ring == 8) && M <= 2) ? o.ring : 4;
   p.waves = std::min(waves, gemv_max_threads(M, p.R, p.D) / 64);
+  // the weight ring in LDS: M = 1, one tile per wave, when the workgroup's LDS fits a CU and the scale tensor is a
+  // whole number of 16-byte pieces (its last piece is loaded whole)
+  if (M == 1 && p.R == 1 && o.lds_ring > 0 && (int64_t)N * (K / 128) % 8 == 0) {
+    p.LR = o.lds_ring;
+    while (p.LR > 4 && gemv_ring_lds(K, K / 128, 16 / p.CS, p.waves, p.LR, true).total > kLdsPerCu) p.LR -= 4;
+    if (gemv_ring_lds(K, K / 128, 16 / p.CS, p.waves, p.LR, true).total > kLdsPerCu) p.LR = 0;
+  }
   return p;
 }
 
@@ -554,6 +672,12 @@ hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
   if (a.norm_w) {                                             // every 32-k block of x held by a thread (2 per thread)
     const int need = (a.K / 32 + 127) / 128;
     while (p.waves < need) p.waves *= 2;
+  }
+  if (p.LR > 0 && a.M == 1 && (int64_t)a.N * (a.K / a.G) % 8 == 0 &&
+      gemv_ring_lds(a.K, a.K / a.G, 16 / p.CS, p.waves, p.LR, a.norm_w).total <= kLdsPerCu) {
+    if (p.CS == 2) return dispatch_lds_ring<2>(a, p.waves, p.LR);
+    if (p.CS == 4) return dispatch_lds_ring<4>(a, p.waves, p.LR);
+    return dispatch_lds_ring<1>(a, p.waves, p.LR);
   }
   switch (a.M) {
     case 1: return dispatch_mfma_layout<1>(a, p.R, p.waves, p.D, p.CS);

@@ -104,6 +104,7 @@ struct GemvPlan {
   int CS = 1;       // workgroups sharing a 16-row tile, 16 / CS rows each (MFMA-layout GEMV, R = 1)
   int TW = 0;       // MFMA GEMM: waves of the one-tile-per-workgroup kernel (0: the row-group kernel)
   int KW = 4;       // MFMA GEMM row groups: tile-waves per K-group (4, or 5, 6, 8 with one tile per wave)
+  int LR = 0;       // M = 1 GEMV: weight ring slots per wave held in LDS (direct-to-LDS loads); 0 = ring in registers
 };
 
 // launch shape of the prefill GEMM (M > 64)
@@ -125,6 +126,7 @@ struct GemvOverride {
   int splits = 0;
   int gemm_kernel = 0;  // MFMA GEMM structure: 0 automatic, 1 row groups (K split across workgroups), 2 one tile each
   int tile_waves = 0;   // MFMA GEMM row groups: tile-waves per K-group (0 automatic, 3, 4, 5, 6 or 8)
+  int lds_ring = 0;     // M = 1 GEMV: 0 automatic, -1 ring in registers, 4 / 8 / 12 / 16 slots per wave in LDS
 };
 GemvOverride gemv_override();
 
@@ -134,6 +136,25 @@ constexpr int gemv_max_threads(int M, int R, int D = 4) {
 }
 
 constexpr size_t kGemvLdsX = 65536;      // x staged in LDS up to this many bytes (the default dynamic LDS limit)
+
+// LDS of the M = 1 GEMV whose weight ring sits in LDS (GemvPlan::LR > 0): x [K] fp16 padded to 1 KB, its zero-weight
+// sums [K / 32][2] fp32, the workgroup's scales [rows][K / G] fp16 padded to 1 KB, the norm weights [K] fp16 padded
+// to 1 KB (fused RMSNorm only), then LR slots of 1 KB per wave. Every direct-to-LDS wave-load writes a whole 1 KB
+// (lanes past the data read zeros), hence the padding.
+struct GemvRingLds {
+  uint32_t xs, s, g, ring, total;
+};
+__host__ __device__ constexpr uint32_t round_1k(uint32_t b) { return (b + 1023u) & ~1023u; }
+__host__ __device__ constexpr GemvRingLds gemv_ring_lds(int K, int KG, int rows, int waves, int LR, bool norm) {
+  GemvRingLds L{};
+  L.xs = round_1k(2u * (uint32_t)K);
+  L.s = L.xs + (uint32_t)(K / 32) * 8u;
+  L.g = L.s + round_1k(2u * (uint32_t)(rows * KG));
+  L.ring = L.g + (norm ? round_1k(2u * (uint32_t)K) : 0u);
+  L.total = L.ring + (uint32_t)(waves * LR) * 1024u;
+  return L;
+}
+constexpr size_t kLdsPerCu = 160 * 1024;  // gfx950
 
 // MFMA GEMM launch shape: K splits across workgroups up to kGemmMaxGroups workgroups (at most kMaxSplits ways), then
 // K-groups inside a workgroup up to kGemmTargetWaves waves. A workspace starts with kCounterBytes of arrival

@@ -207,9 +207,10 @@ def prefill_path(m, wq):
 
 def linear(x, wq, max_gemv_rows=8, version=0, bias=None):
     """Decode (few rows): an INT4 kernel (v6 GEMV for one row, v5 MFMA beyond). Prefill (many rows): dequantize, then
-    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM where prefill_path says (long K,
-    up to 256 rows, small layers up to 512 rows). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row limit) rows (v5:
-    64), and dequantize + BLAS above.
+    the fp16 BLAS GEMM (hipBLASLt under PyTorch-ROCm), or the int4 prefill GEMM where prefill_path says (K >=
+    AUTO_PREFILL_MIN_K at any M, every layer up to AUTO_PREFILL_ROWS rows, layers with N and K <= AUTO_PREFILL_NARROW
+    up to AUTO_PREFILL_NARROW_ROWS rows). version 0 = auto; a fixed version runs up to min(max_gemv_rows, its row
+    limit) rows (v5: 64), and dequantize + BLAS above.
     bias ([N], optional; not in the reference's signature; used in fp16 on x's device on every route): y =
     fp16(x W^T) + bias in fp16, the rounding of the reference's linear() followed by `+ bias`; the v5, one-row v6 and prefill kernels add it in their store (no extra
     launch), multi-row v6 and dequantize + BLAS with a separate add."""

@@ -285,6 +285,36 @@ def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
     assert int(torch.count_nonzero(ws[:4096])) == 0
 
 
+@pytest.mark.parametrize("hq,hkv,L,positions", [(12, 2, 300, [63, 64, 65]), (16, 2, 600, list(range(100, 148))),
+                                                (28, 4, 2048, list(range(5, 40))), (16, 2, 4096, list(range(700, 716)))])
+@pytest.mark.parametrize("poison", [float("nan"), float("inf")])
+def test_attention_ignores_unwritten_cache_rows(cuda, hq, hkv, L, positions, poison):
+    """Cache rows past the step's last position are never attended: filled with NaN or Inf (an uninitialized cache),
+    they leave every output finite and equal to the fp32 softmax over the written rows -- on the decode kernel (few
+    query rows per KV head) and on the MFMA kernel (32 or more), with and without key partitions."""
+    g = torch.Generator(device="cuda").manual_seed(L + len(positions))
+    m = len(positions)
+    q = torch.randn(m, hq, 128, generator=g, device="cuda").half()
+    k_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
+    v_cache = torch.randn(hkv, L, 128, generator=g, device="cuda").half()
+    last = max(positions)
+    k_cache[:, last + 1:] = poison
+    v_cache[:, last + 1:] = poison
+    pos = torch.tensor(positions, device="cuda")
+    scale = 1 / math.sqrt(128)
+    grp = hq // hkv
+    ref = torch.empty(m, hq, 128, dtype=torch.float32, device="cuda")
+    for i, p in enumerate(positions):
+        for h in range(hq):
+            kk, vv = k_cache[h // grp, :p + 1].float(), v_cache[h // grp, :p + 1].float()
+            ref[i, h] = torch.softmax(kk @ q[i, h].float() * scale, 0) @ vv
+    for split in (False, True):
+        out = torch.empty(m, hq * 128, dtype=torch.half, device="cuda")
+        ops.ext().attention(q, k_cache, v_cache, pos, out, hq, hkv, L, scale, split=split)
+        assert bool(torch.isfinite(out).all()), split
+        assert rel(out.view(m, hq, 128), ref.double()) < 3e-3, split
+
+
 @pytest.fixture(scope="module")
 def tiny_models():
     torch.cuda.set_device(0)

@@ -183,21 +183,52 @@ def test_dispatch_matrix(cuda):
             e = rel(ops.linear(x, wq), x.double() @ ref_w.T)
             worst = max(worst, e)
             assert e <= R.REL_BOUND, (name, m, ops.auto_version(m, wq), e)
-    wq = ops.W4Weight.from_float(torch.randn(256, 512))
-    x = torch.randn(9, 512).half().cuda()
-    assert bool(torch.isfinite(ops.linear(x, wq, max_gemv_rows=16, version=6)).all())      # v6 takes 8: falls back
-    s = torch.cuda.Stream()
-    with torch.cuda.stream(s):
-        y_side = ops.linear(x[:1], wq)
-    s.synchronize()
-    assert torch.equal(y_side, ops.linear(x[:1], wq))
-    for bad in (lambda: ops.ext().w4_dequant(wq.packed, wq.scales.cpu(), 128),           # CPU scales
-                lambda: ops.ext().w4_gemv(x[:1], wq.packed, wq.scales, 0, 1, 0),          # group 0
-                lambda: ops.ext().w4_gemv(x, wq.packed, wq.scales, 128, 1, 0),            # 9 rows into a GEMV
-                lambda: ops.ext().w4_gemm_tc(torch.zeros(65, 512, dtype=torch.half, device="cuda"), wq.packed_mma,
-                                             wq.scales, 128)):                            # 65 rows into v5
-        with pytest.raises(RuntimeError):
-            bad()
+
+
+def test_fixed_versions_past_their_rows_take_the_dequant_route(cuda):
+    """A fixed version asked for more rows than it serves (v6: min(max_gemv_rows, 8); v5: 64) runs the dequantize +
+    BLAS route: the same bits as F.linear on ops.dequant's fp16 weight, and within the bound of the fp64 product."""
+    wq, ref_w, *_, gen = make_weight(768, 320, 41, layouts=("canonical", "mma"))
+    w16 = ops.dequant(wq, "mma")
+    for version, m, cap in ((6, 9, 16), (6, 5, 4), (5, 65, 8), (2, 12, 8)):
+        x = torch.randn(m, 768, generator=gen).half().cuda()
+        y = ops.linear(x, wq, max_gemv_rows=cap, version=version)
+        assert torch.equal(y, torch.nn.functional.linear(x, w16)), (version, m)
+        assert rel(y, x.double() @ ref_w.T) <= R.REL_BOUND, (version, m)
+
+
+def test_results_do_not_depend_on_the_stream(cuda):
+    """Every route gives the same bits on two side streams as on the default stream (the binding launches on the
+    current stream and keeps one workspace per stream)."""
+    wq, *_, gen = make_weight(2048, 1024, 43, layouts=("mma",))
+    xs = [torch.randn(m, 2048, generator=gen).half().cuda() for m in (1, 3, 24, 64, 200)]
+    want = [ops.linear(x, wq) for x in xs]
+    for side in (torch.cuda.Stream(), torch.cuda.Stream()):
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            got = [ops.linear(x, wq) for x in xs]
+        side.synchronize()
+        for x, a, b in zip(xs, got, want):
+            assert torch.equal(a, b), x.shape[0]
+
+
+@pytest.mark.parametrize("case", ["scales_on_host", "group_zero", "nine_rows_gemv", "rows_past_v5", "version_7"])
+def test_malformed_calls_raise_with_the_reason(cuda, case):
+    """The extension refuses malformed calls with RuntimeError naming the problem (the reference's TORCH_CHECKs)."""
+    wq = ops.W4Weight.from_float(torch.randn(96, 256))
+    x1, x9 = torch.randn(1, 256).half().cuda(), torch.randn(9, 256).half().cuda()
+    ext = ops.ext()
+    calls = {
+        "scales_on_host": (lambda: ext.w4_dequant(wq.packed, wq.scales.cpu(), 128), "same GPU"),
+        "group_zero": (lambda: ext.w4_gemv(x1, wq.packed, wq.scales, 0, 1, 0), "group size must be positive"),
+        "nine_rows_gemv": (lambda: ext.w4_gemv(x9, wq.packed, wq.scales, 128, 2, 0), "1..8 rows"),
+        "rows_past_v5": (lambda: ext.w4_gemm_tc(torch.zeros(65, 256, dtype=torch.half, device="cuda"),
+                                                wq.packed_mma, wq.scales, 128), "1..64 rows"),
+        "version_7": (lambda: ext.w4_gemv(x1, wq.packed, wq.scales, 128, 7, 0), "version"),
+    }
+    call, reason = calls[case]
+    with pytest.raises(RuntimeError, match=reason):
+        call()
 
 
 def test_graph_capture_replays_match_eager(cuda):

@@ -8,6 +8,7 @@ rule other than half-to-even, a scale rounded twice) fails it.
 """
 import fractions
 import pathlib
+import struct
 
 import numpy as np
 import pytest
@@ -18,8 +19,15 @@ GOLDEN = np.load(pathlib.Path(__file__).resolve().parent / "golden" / "w4_golden
 CASES = sorted({k[:-5] for k in GOLDEN.files if k.endswith("_meta")})
 
 
-def words_of(packed):
-    return np.ascontiguousarray(packed).view("<u4")
+def assemble_le32(b):
+    """uint8 [N, 4 W] -> uint32 [N, W]: byte 4 i + j of a row is bits 8 j .. 8 j + 7 of word i (little-endian),
+    computed arithmetically rather than through a dtype view."""
+    b = np.asarray(b, np.uint32).reshape(b.shape[0], -1, 4)
+    return b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16) | (b[..., 3] << 24)
+
+
+def place(words, row, word, slot, value):
+    words[row, word] |= np.uint32(int(value) << (4 * slot))
 
 
 # ---- known answers from the reference's tests ----
@@ -31,10 +39,16 @@ def test_kat_two_nibbles_per_byte_low_first():
 
 
 def test_kat_magic_number():
-    u = GOLDEN["kat_magic_u"]
-    h = (u | 0x6400).view(np.float16)
-    assert np.array_equal(h.astype(np.float32) - 1032.0, GOLDEN["kat_magic_value"])
-    assert np.array_equal(h - np.float16(1032), GOLDEN["kat_magic_value"].astype(np.float16))
+    """binary16 0x6400 is 2^10, where the mantissa step is exactly 1: a nibble u in mantissa bits 0..3 reads as
+    1024 + u, in bits 4..7 as 1024 + 16 u; subtracting 1032 from the first leaves u - 8 with no rounding (every
+    operand and result is an integer below 2^11). Decoded with the standard library's binary16 codec."""
+    def half(bits):
+        return struct.unpack("<e", struct.pack("<H", bits))[0]
+    for u, want in zip(GOLDEN["kat_magic_u"].tolist(), GOLDEN["kat_magic_value"].tolist()):
+        assert half(0x6400 | u) == 1024 + u
+        assert half(0x6400 | (u << 4)) == 1024 + 16 * u
+        assert half(0x6400 | u) - 1032 == want
+        assert float(np.float16(half(0x6400 | u)) - np.float16(1032)) == want
 
 
 def test_kat_overflow_case_closed_form():
@@ -87,68 +101,102 @@ def test_quantize_brute_force_nearest_level():
             assert q[n, k] == want
 
 
-def test_error_is_at_most_half_a_step():
-    rng = np.random.default_rng(103)
-    w = rng.standard_normal((64, 512)).astype(np.float32)
+def test_reconstruction_within_half_a_step_under_heavy_tails():
+    """Absmax scaling never clips: with a heavy-tailed weight (a few outliers set each group's scale) every weight is
+    within half a step of code * scale, checked in fp64 per element."""
+    rng = np.random.default_rng(203)
+    w = (rng.standard_t(3, (40, 768)) * 0.3).astype(np.float32)
     packed, scales = R.quantize_w4(w, 128)
-    err = np.abs(R.dequantize_w4(packed, scales, 128) - w).reshape(64, 4, 128)
-    assert np.all(err <= scales.astype(np.float32)[..., None] / 2 + 1e-6)
+    step = np.repeat(scales.astype(np.float64), 128, axis=1)
+    codes = R.unpack_w4(packed).astype(np.float64)
+    assert float(np.max(np.abs(w.astype(np.float64) - codes * step) / step)) <= 0.5 + 1e-6
 
 
-def test_range_and_zero_group():
-    rng = np.random.default_rng(104)
-    w = rng.standard_normal((8, 256)).astype(np.float32) * 50
-    w[3] = 0
+def test_group_peak_takes_the_end_code_and_zero_groups_are_exact():
+    """The largest-magnitude weight of a group maps to +7 or -7 with its sign (amax / fp16(amax / 7) is 7 to within
+    fp16 rounding); a group of zeros gets scale 1.0 and code 0 throughout, so it dequantizes to exact zeros; no code
+    leaves -8..7."""
+    rng = np.random.default_rng(204)
+    w = (rng.standard_normal((10, 512)) * 40).astype(np.float32)
+    w[4, 256:384] = 0.0
     packed, scales = R.quantize_w4(w, 128)
-    q = R.unpack_w4(packed)
-    assert q.min() >= -8 and q.max() <= 7
-    assert np.all(scales[3] == 1.0) and np.all(R.dequantize_w4(packed, scales, 128)[3] == 0)
+    q = R.unpack_w4(packed).reshape(10, 4, 128)
+    g = w.reshape(10, 4, 128)
+    for n in range(10):
+        for gi in range(4):
+            if (n, gi) == (4, 2):
+                continue
+            i = int(np.abs(g[n, gi]).argmax())
+            assert int(q[n, gi, i]) == (7 if g[n, gi, i] > 0 else -7), (n, gi)
+    assert scales[4, 2] == 1.0 and not q[4, 2].any()
+    assert not R.dequantize_w4(packed, scales, 128)[4, 256:384].any()
+    assert int(q.min()) >= R.QMIN and int(q.max()) <= R.QMAX
 
 
-def test_rejects_bad_shapes():
+@pytest.mark.parametrize("call", [
+    lambda: R.quantize_w4(np.zeros((2, 200), np.float32), 64),      # K not a multiple of G
+    lambda: R.quantize_w4(np.zeros((2, 160), np.float32), 80),      # G not a multiple of 32
+    lambda: R.quantize_w4(np.zeros((2, 96), np.float32), 128),      # K smaller than one group
+    lambda: R.interleave_for_mma(np.zeros((2, 96), np.uint8)),      # K = 192: not whole 128-k chunks
+    lambda: R.interleave_for_mfma(np.zeros((3, 32), np.uint8)),     # K = 64
+])
+def test_shapes_outside_the_format_raise(call):
     with pytest.raises(ValueError):
-        R.quantize_w4(np.zeros((4, 100), np.float32), 128)
-    with pytest.raises(ValueError):
-        R.quantize_w4(np.zeros((4, 96), np.float32), 48)
-    with pytest.raises(ValueError):
-        R.interleave_for_mma(np.zeros((1, 32), np.uint8))
-    with pytest.raises(ValueError):
-        R.interleave_for_mfma(np.zeros((1, 32), np.uint8))
+        call()
 
 
-# ---- layouts: bit logic simulated lane by lane ----
+# ---- layouts: each value placed where the specification puts it (packing direction) ----
 
-def test_canonical_words_v2_bit_logic():
-    rng = np.random.default_rng(105)
-    packed, _ = R.quantize_w4(rng.standard_normal((5, 256)).astype(np.float32))
-    u = R.unpack_w4(packed) + 8
-    words = words_of(packed)
-    for b in range(8):
-        assert np.array_equal((words >> (4 * b)) & 0xF, u[:, b::8])
-
-
-def test_v3_words_bit_logic():
-    rng = np.random.default_rng(106)
-    packed, _ = R.quantize_w4(rng.standard_normal((5, 256)).astype(np.float32))
-    u = R.unpack_w4(packed) + 8
-    words = words_of(R.interleave_for_gpu(packed)).astype(np.uint64)
-    for j in range(4):
-        t = (words >> (4 * j)) & 0x000F000F
-        assert np.array_equal(t & 0xFFFF, u[:, 2 * j::8])
-        assert np.array_equal(t >> 16, u[:, 2 * j + 1::8])
+def _random_codes(seed, n, k):
+    """Nibbles u in 0..15 and the canonical bytes holding them, packed by definition (byte j: u[2 j] low nibble,
+    u[2 j + 1] high nibble)."""
+    u = np.random.default_rng(seed).integers(0, 16, (n, k))
+    canon = np.zeros((n, k // 2), np.uint8)
+    for row in range(n):
+        for kk in range(k):
+            canon[row, kk // 2] |= np.uint8(int(u[row, kk]) << (4 * (kk % 2)))
+    return u, canon
 
 
-def test_nv_mma_layout_feeds_each_lane_its_fragment():
-    rng = np.random.default_rng(5)
-    packed, _ = R.quantize_w4(rng.standard_normal((3, 384)).astype(np.float32))
-    u = R.unpack_w4(packed) + 8
-    words = R.interleave_for_mma(packed).reshape(3, -1, 4, 4, 4).view("<u4")[..., 0]
-    for c in range(3):
-        for t in range(4):
-            for s in range(16):
-                w, j = int(words[1, c, t, s >> 2]), s & 3
-                k = 128 * c + 8 * s + 2 * t
-                assert (w >> (4 * j)) & 0xF == u[1, k] and (w >> (4 * j + 16)) & 0xF == u[1, k + 1]
+def test_canonical_words_place_value_k_at_nibble_k_mod_8():
+    """In the canonical layout read as little-endian words, value k sits in word k // 8 at nibble k % 8, and the
+    oracle's unpack recovers every value."""
+    u, canon = _random_codes(205, 5, 256)
+    words = np.zeros((5, 32), np.uint32)
+    for row in range(5):
+        for k in range(256):
+            place(words, row, k // 8, k % 8, u[row, k])
+    assert np.array_equal(assemble_le32(canon), words)
+    assert np.array_equal(R.unpack_w4(canon).astype(np.int64) + 8, u)
+
+
+def test_v3_words_place_even_values_low_and_odd_values_high():
+    """v3 order: value k0 + p of a word goes to nibble slot p / 2 when p is even (low half) and 4 + (p - 1) / 2
+    when odd (high half), so a (k0 + 2 j, k0 + 2 j + 1) pair lands in the two 16-bit halves at the same shift."""
+    u, canon = _random_codes(206, 5, 256)
+    words = np.zeros((5, 32), np.uint32)
+    for row in range(5):
+        for k in range(256):
+            p = k % 8
+            place(words, row, k // 8, p // 2 + 4 * (p % 2), u[row, k])
+    assert np.array_equal(assemble_le32(R.interleave_for_gpu(canon)), words)
+
+
+def test_nv_mma_words_hold_the_fragment_pairs():
+    """NVIDIA m16n8k8 order: word i of 16-byte group t of 128-k chunk c holds, in nibble pair j, the values
+    k = 128 c + 32 i + 8 j + 2 t (low half) and k + 1 (high half)."""
+    n, k_dim = 4, 512
+    u, canon = _random_codes(207, n, k_dim)
+    words = np.zeros((n, k_dim // 8), np.uint32)
+    for row in range(n):
+        for c in range(k_dim // 128):
+            for t in range(4):
+                for i in range(4):
+                    for j in range(4):
+                        k = 128 * c + 32 * i + 8 * j + 2 * t
+                        place(words, row, 16 * c + 4 * t + i, j, u[row, k])
+                        place(words, row, 16 * c + 4 * t + i, 4 + j, u[row, k + 1])
+    assert np.array_equal(assemble_le32(R.interleave_for_mma(canon)), words)
 
 
 @pytest.mark.parametrize("n", [1, 5, 16, 21, 37])
