@@ -100,6 +100,11 @@ def parse():
                          "tokens (a profiler workload; prints nothing else)")
     ap.add_argument("--chunk", type=int, default=1,
                     help="with --decode-trace: tokens fed per captured step (1 = greedy decoding)")
+    ap.add_argument("--no-decode", action="store_true", help="skip the configs[4] decode block")
+    ap.add_argument("--no-trace", action="store_true",
+                    help="skip the traced run of the timed workload (roofline from graph time per launch instead)")
+    ap.add_argument("--trace-child", action="store_true",
+                    help="(internal) the timed workload alone, run by the parent under rocprofv3 --kernel-trace")
     ap.add_argument("--out", default=None)
     return ap.parse_args()
 
@@ -311,11 +316,14 @@ def shape_detail(torch, ops, projs, pool, xs, peak=None):
     return out
 
 
-# the 7B-shaped MLP projections the per-shape table adds to the step's 1.5B / 3B shapes
-SHAPES_7B = [("7b.gate", 3584, 18944), ("7b.down", 18944, 3584)]
-# the skinny block of the default line: (name, K, N) x M (the M = 2..64 half of the metric)
-SKINNY_BLOCK = [("3b.gate_up", 2048, 11008), ("7b.down", 18944, 3584)]
-SKINNY_BLOCK_M = (2, 16, 32, 64)
+# the shapes the per-shape table adds to the step's 1.5B / 3B shapes: BASELINE configs[0]'s Qwen2.5-0.5B gate/up
+# and the 7B-shaped MLP projections of configs[2]
+SHAPES_EXTRA = [("0.5b.gate_up", 896, 4864), ("7b.gate", 3584, 18944), ("7b.down", 18944, 3584)]
+# the skinny block of the default line: every (shape, M) of BASELINE configs[2] above M = 1 (the M = 2..64 half of
+# the metric; M = 1 is per_shape)
+SKINNY_BLOCK = [("3b.gate_up", 2048, 11008), ("3b.down", 11008, 2048), ("7b.gate_up", 3584, 18944),
+                ("7b.down", 18944, 3584)]
+SKINNY_BLOCK_M = (2, 4, 8, 16, 24, 32, 48, 64)
 MFMA_F16_PEAK_TFLOPS = 2500.0               # MI355X dense fp16 MFMA
 
 
@@ -359,10 +367,10 @@ def provenance(torch, ops):
 
 
 def skinny_block(torch, ops):
-    """The M = 2..64 half of the metric on the 3B gate/up and 7B down shapes: us per call of the
-    MFMA kernel (v5), dequantize + hipBLASLt and fp16 hipBLASLt, each a graph over >= 1 GiB of cold copies (int4 for
-    the first two, fp16 for the last); the v5 kernel's algorithmic bandwidth and its MFMA utilisation (2 M N K / t
-    against the 2.5 PFLOP/s dense fp16 peak)."""
+    """The M = 2..64 half of the metric (the 3B and 7B-shaped MLP projections at M = 2, 4, 8,
+    16, 24, 32, 48, 64): us per call of the MFMA kernel (v5), dequantize + hipBLASLt and fp16 hipBLASLt, each a graph
+    over >= 1 GiB of cold copies (int4 for the first two, fp16 for the last); the v5 kernel's algorithmic bandwidth
+    and its MFMA utilisation (2 M N K / t against the 2.5 PFLOP/s dense fp16 peak)."""
     rows = []
     for name, k, n in SKINNY_BLOCK:
         pool, pool16, _, copies = build_pool(torch, ops, [(name, k, n)], fp16=True, seed=k + n)
@@ -383,11 +391,120 @@ def skinny_block(torch, ops):
     return rows
 
 
-def per_shape_7b(torch, ops, peak=None):
-    """The 7B-shaped projections, per call like shape_detail, on one clip-searched weight cloned into >= 1 GiB."""
+# BASELINE configs[4] in the default line: a 512-token prompt, greedy tokens and tokens fed 16 / 48 per step
+DECODE_BLOCK = dict(model="3b", prompt=512, new=128, feed=192, chunks=(16, 48))
+
+
+def decode_block(torch, ops):
+    """Batch-1 decode of a random-init Qwen2.5-3B architecture, every step one hipGraph replay:
+    * fused layers (lowbit.fused, 5 launches per layer for one token) with W4A16 projections (int4 g128, clip search),
+      with fp16 projections through the library's fp16-weight GEMV (the same kernel structure, epilogues and fusions:
+      only the weight bytes differ; multi-token steps use hipBLASLt), and with fp16 projections through hipBLASLt;
+    * transformers' own modules with fp16 nn.Linear and with the W4Linear drop-in (the reference's comparison,
+      bench/e2e.py:84-147), greedy only.
+    Per variant: TTFT (median of 3 eager prefills of the prompt), greedy ms/token (one warm-up run, then the timed
+    run), tokens/s fed `chunks` tokens per step; bytes per greedy token (projection weights + tied head + the KV rows
+    read at the mean position) and that over the step time. Speed-ups W4A16 / fp16 both ways."""
+    from lowbit import decode, fused, model as lbmodel
+    cfg = DECODE_BLOCK
+    m = decode.random_model(cfg["model"], seed=0)
+    mc = m.config
+    vocab, hidden, layers = mc.vocab_size, mc.hidden_size, mc.num_hidden_layers
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    prompt = torch.randint(0, vocab, (1, cfg["prompt"]), generator=gen, device="cuda")
+    feed = torch.randint(0, vocab, (cfg["feed"],), generator=gen, device="cuda")
+    max_len = cfg["prompt"] + max(cfg["new"], cfg["feed"]) + 64
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    mean_pos = cfg["prompt"] + cfg["new"] / 2
+    kv_bytes = layers * 2 * mc.num_key_value_heads * 128 * 2 * mean_pos
+    head_bytes = vocab * hidden * 2
+
+    def timed(fn):
+        e0, e1 = ev(), ev()
+        e0.record()
+        r = fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1), r
+
+    def run(make, chunks, weight_bytes):
+        dec = make(1)
+        ttft = sorted(timed(lambda: dec.prefill(prompt).argmax(-1))[0] for _ in range(3))[1]
+        dec.capture()
+        for _ in range(2):                                   # a warm-up run, then the timed one
+            first = dec.prefill(prompt).argmax(-1)
+            ms, _ = timed(lambda: dec.greedy(first, cfg["new"]))
+        del dec
+        per_tok = ms / (cfg["new"] - 1)
+        step_bytes = weight_bytes + head_bytes + kv_bytes
+        r = {"ttft_ms": round(ttft, 3), "greedy_ms_per_token": round(per_tok, 4),
+             "greedy_tokens_per_s": round(1000 / per_tok, 1), "bytes_per_token": int(step_bytes),
+             "bytes_per_token_TBps": round(step_bytes / (per_tok * 1e-3) / 1e12, 3)}
+        for c in chunks:
+            dc = make(c)
+            dc.prefill(prompt)
+            dc.capture()
+            best = 1e30
+            for _ in range(2):
+                dc.prefill(prompt)
+                t, _ = timed(lambda: [dc.step(feed[i:i + c]) for i in range(0, cfg["feed"], c)])
+                best = min(best, t)
+            r[f"feed_{c}_tokens_per_s"] = round(cfg["feed"] / (best / 1000), 1)
+            del dc
+        torch.cuda.empty_cache()
+        return r
+
+    def fused_bytes(fq):
+        b = 0
+        for lay in fq.layers:
+            for name in ("qkv", "o", "gu", "down"):
+                pj = lay[name]
+                b += pj.wq.nbytes() if hasattr(pj, "wq") else pj.w.numel() * 2
+        return b
+
+    out = {}
+    fq = fused.FusedQwen2(m, max_len, quant="int4", clip_grid=CLIP_GRID)
+    out["fused_int4"] = run(lambda c: fused.FusedDecoder(fq, c), cfg["chunks"], fused_bytes(fq))
+    del fq
+    fq = fused.FusedQwen2(m, max_len, quant="fp16_gemv")
+    out["fused_fp16_gemv"] = run(lambda c: fused.FusedDecoder(fq, c), cfg["chunks"], fused_bytes(fq))
+    del fq
+    fq = fused.FusedQwen2(m, max_len, quant="fp16")
+    out["fused_fp16_hipblaslt"] = run(lambda c: fused.FusedDecoder(fq, c), cfg["chunks"], fused_bytes(fq))
+    del fq
+    torch.cuda.empty_cache()
+    linear_bytes = sum(mod.weight.numel() * 2 for name, mod in m.model.layers.named_modules()
+                       if name.split(".")[-1] in lbmodel.TARGETS)
+    out["hf_fp16"] = run(lambda c: decode.GraphDecoder(m, max_len, c), (), linear_bytes)
+    layers_q = lbmodel.quantize_layers(m, GROUP, CLIP_GRID)
+    _, int4_bytes = lbmodel.apply_int4(layers_q)
+    out["hf_w4linear"] = run(lambda c: decode.GraphDecoder(m, max_len, c), (), int4_bytes)
+    del m, layers_q
+    torch.cuda.empty_cache()
+
+    def sp(a, b, key):
+        return round(out[b][key] / out[a][key], 3) if key.startswith("greedy_ms") else round(out[a][key] / out[b][key], 3)
+    keys = ["greedy_ms_per_token"] + [f"feed_{c}_tokens_per_s" for c in cfg["chunks"]]
+    return {"workload": f"BASELINE configs[4]: random-init Qwen2.5-{cfg['model']} architecture (no checkpoint), "
+                        f"{cfg['prompt']}-token uniform-random prompt, {cfg['new']} greedy tokens, {cfg['feed']} "
+                        f"tokens fed {'/'.join(map(str, cfg['chunks']))} per step; int4 g128 with the clip search",
+            "variants": out,
+            "speedup_w4a16": {
+                "fused_int4_over_fused_fp16_gemv": {k: sp("fused_int4", "fused_fp16_gemv", k) for k in keys},
+                "fused_int4_over_fused_fp16_hipblaslt": {k: sp("fused_int4", "fused_fp16_hipblaslt", k) for k in keys},
+                "hf_w4linear_over_hf_fp16": {"greedy_ms_per_token": sp("hf_w4linear", "hf_fp16",
+                                                                       "greedy_ms_per_token")},
+                "fused_int4_over_hf_fp16": {"greedy_ms_per_token": sp("fused_int4", "hf_fp16",
+                                                                      "greedy_ms_per_token")}},
+            "ttft_ms": {k: v["ttft_ms"] for k, v in out.items()}}
+
+
+def per_shape_extra(torch, ops, peak=None):
+    """The configs[0] and 7B-shaped projections, per call like shape_detail, on one clip-searched weight cloned into
+    >= 1 GiB."""
     out = {}
     gen = torch.Generator(device="cuda").manual_seed(7)
-    for name, k, n in SHAPES_7B:
+    for name, k, n in SHAPES_EXTRA:
         w = torch.randn(n, k, generator=gen, device="cuda") * 0.02
         packed, scales = ops.quantize_w4_gpu(w, GROUP, CLIP_GRID)
         base = ops.W4Weight(packed, scales, GROUP, ("mma",), device=packed.device)
@@ -410,8 +527,86 @@ def per_shape_workload(a):
     gen = torch.Generator(device="cuda").manual_seed(1)
     xs = {name: torch.randn(1, k, generator=gen, device="cuda").half() for name, k, n in projs}
     detail = shape_detail(torch, ops, projs, pool, xs)
-    detail.update(per_shape_7b(torch, ops))
+    detail.update(per_shape_extra(torch, ops))
     print(json.dumps({"per_shape_workload": True, "per_shape": detail}), flush=True)
+
+
+GEMV_KERNEL = "gemv_mfma_layout"
+
+
+def progress(msg):
+    """A stage finished (stderr: stdout carries only the JSON line)."""
+    print(f"[bench] {msg} ({time.strftime('%H:%M:%S')})", file=sys.stderr, flush=True)
+
+
+def traced_gemv(a):
+    """The timed workload (this script with --trace-child: pool, warm-up, capture, one untimed and `replays` timed
+    replays of the K-step graph) run under `rocprofv3 --kernel-trace`, before this process touches the GPU. Returns
+    the durations of the GEMV dispatches of the timed replays (the last replays x steps x 14 of them) from the trace's
+    own start / end stamps, the traced replays' wall time per launch (first start to last end: the tracer's gaps
+    between dispatches), and per-instance averages; None when rocprofv3 is missing or the run fails."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3") else None)
+    if prof is None:
+        return None
+    tmp = tempfile.mkdtemp(prefix="lowbit_trace_")
+    cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "head", "--", sys.executable, "-u",
+           str(ROOT / "bench.py"), "--trace-child", "--steps", str(a.steps), "--warmup", str(a.warmup), "--replays",
+           str(a.replays)]
+    try:
+        subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=600, cwd="/tmp",
+                       env={**os.environ, "TMPDIR": "/tmp"})
+    except (OSError, subprocess.SubprocessError):
+        pass                        # the profiler may end abnormally after a complete trace: the files decide
+    rows = []
+    for path in glob.glob(os.path.join(tmp, "**", "*kernel_trace.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if GEMV_KERNEL in r.get("Kernel_Name", ""):
+                    rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    shutil.rmtree(tmp, ignore_errors=True)
+    n = a.replays * a.steps * len(step_projections())
+    if len(rows) < n:
+        return None
+    rows = sorted(rows)[-n:]
+    dur = [(e - b) / 1000 for b, e, _ in rows]
+    last = rows[-a.steps * len(step_projections()):]        # the final replay alone
+    per = {}
+    for (b, e, name), d in zip(rows, dur):
+        key = name[name.find(GEMV_KERNEL):].split("(")[0]   # the instance: template arguments
+        per.setdefault(key, []).append(d)
+    return {"avg_us": sum(dur) / len(dur), "dispatches": len(dur),
+            "traced_wall_us_per_launch": (last[-1][1] - last[0][0]) / 1000 / len(last),
+            "instances": {k: {"calls": len(v), "avg_us": round(sum(v) / len(v), 3)} for k, v in sorted(per.items())}}
+
+
+def roofline(trace, bytes_per_launch, graph_us, launches):
+    """The GEMV kernel's roofline entry. With a trace, its average launch duration is the traced kernel duration
+    (each dispatch timed alone by the profiler: the conservative figure, reproducible from a rocprofv3 summary of the
+    same command); the untimed-graph figure, elapsed / launches (back-to-back launches overlap their dispatch), is
+    kept beside it. Without one, the graph figure."""
+    avg = trace["avg_us"] if trace else graph_us
+    r = {"bound": "hbm", "achieved": round(bytes_per_launch / (avg * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+         "unit": "GB/s", "frac": round(bytes_per_launch / (avg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+         "traffic": TRAFFIC_PER_LAUNCH,
+         # one kernel template, three instances by layer: whole 16-row tiles (CS = 1: the 1.5B q/k/v/o and both
+         # models' gate/up), tiles split over 2 workgroups (3B q/o, both downs) or 4 (3B k/v)
+         "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false,CS>, CS = 1 / 2 / 4",
+         "kernel_avg_us": round(avg, 3), "bytes_per_launch_avg": bytes_per_launch, "launches": launches,
+         "kernel_avg_source": ("rocprofv3 --kernel-trace of the same timed workload (bench.py --trace-child), "
+                               "mean duration of the timed replays' GEMV dispatches" if trace else
+                               "graph elapsed / launches (no trace)"),
+         "graph_us_per_launch": round(graph_us, 3),
+         "graph_achieved": round(bytes_per_launch / (graph_us * 1e-6) / 1e9, 1),
+         "frac_graph": round(bytes_per_launch / (graph_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    if trace:
+        r["trace"] = {"dispatches": trace["dispatches"], "instances": trace["instances"],
+                      "traced_wall_us_per_launch": round(trace["traced_wall_us_per_launch"], 3)}
+    return r
 
 
 def contract(a):
@@ -477,11 +672,16 @@ def contract(a):
             for name, k, n in projs:
                 torch.nn.functional.linear(xs[name], layer[name])
         fp16 = graph_time_us(torch, step16, a.steps, reps=1) / 1000
+    progress(f"timed region done: {value:.1f} GB/s")
     peak = None if a.no_detail else measured_peak(torch, ops)
     detail = None if a.no_detail else shape_detail(torch, ops, projs, pool, xs, peak["read_gbps"])
     if detail is not None:
-        detail.update(per_shape_7b(torch, ops, peak["read_gbps"]))
+        detail.update(per_shape_extra(torch, ops, peak["read_gbps"]))
+    progress("per-shape table done")
     skinny = None if a.no_detail else skinny_block(torch, ops)
+    progress("skinny table done")
+    decode_line = None if (a.no_detail or a.no_decode) else decode_block(torch, ops)
+    progress("decode block done")
     by_step = sorted(step_bytes / (t / a.steps / 1e3) / 1e9 for t in replay_ms)
 
     line = {
@@ -501,14 +701,7 @@ def contract(a):
         "config": {"workload": "BASELINE configs[1]: M=1 GEMV over the 7 projections of one Qwen2.5-1.5B and one "
                                "Qwen2.5-3B decoder layer per step (14 launches), hipGraph replay",
                    "step_bytes": step_bytes, "M": 1, "group": GROUP, "parallelism": "single GPU"},
-        # the timed graph holds only the M=1 GEMV kernel, so its average launch duration is elapsed / launches
-        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBPS, 4), "traffic": TRAFFIC_PER_LAUNCH,
-                     # one kernel template, three instances by layer: whole 16-row tiles (CS = 1: the 1.5B q/k/v/o
-                     # and both models' gate/up), tiles split over 2 workgroups (3B q/o, both downs) or 4 (3B k/v)
-                     "kernel": "lowbit::gemv_mfma_layout<1,1,4,true,false,CS>, CS = 1 / 2 / 4",
-                     "kernel_avg_us": round(1000 * elapsed_ms / launches, 3), "launches": launches,
-                     "bytes_per_launch_avg": step_bytes // len(projs)},
+        "roofline": roofline(a.trace, step_bytes // len(projs), 1000 * elapsed_ms / launches, launches),
         "replays": {"n": len(replay_ms), "ms_per_step": [round(t / a.steps, 4) for t in replay_ms],
                     "GBps_median": round(by_step[len(by_step) // 2], 1), "GBps_min": round(by_step[0], 1),
                     "GBps_max": round(by_step[-1], 1)},
@@ -518,11 +711,12 @@ def contract(a):
         "measured_peak": peak,
         "per_shape": detail,
         "skinny": skinny,
+        "decode": decode_line,
         "provenance": provenance(torch, ops),
     }
     if peak:
         line["roofline"]["measured_peak_gbps"] = peak["read_gbps"]
-        line["roofline"]["frac_of_measured_peak"] = round(value / peak["read_gbps"], 4)
+        line["roofline"]["frac_of_measured_peak"] = round(line["roofline"]["achieved"] / peak["read_gbps"], 4)
     if not a.no_cpu:
         line["cpu_baseline"] = cpu_baseline(projs, host, xs)
     print(json.dumps(line), flush=True)
@@ -1088,7 +1282,14 @@ def main():
         decode_trace(a)
     elif a.e2e:
         e2e(a)
+    elif a.trace_child:
+        a.no_cpu = a.no_fp16 = a.no_detail = True
+        a.trace = None
+        contract(a)
     else:
+        # the traced run first, while this process has not touched the GPU
+        a.trace = None if a.no_trace else traced_gemv(a)
+        progress("traced run " + ("done" if a.trace else "unavailable: roofline from graph time"))
         contract(a)
 
 

@@ -197,6 +197,20 @@ int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, i
                        const float* inv_freq, void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv,
                        int64_t L, void* stream);
 
+/* lowbit_w4_linear_fused for one row over an fp16 weight w [N, K] (row-major, 16-byte aligned; K % 128 == 0, at
+ * most 16384): the W4A16 decode's fp16 comparator, with the same kernel structure, epilogues (store, bias, residual,
+ * silu-mul on 8 / 8 interleaved rows) and fused input RMSNorm, so that the two differ only in the weight bytes they
+ * stream. fp16 products summed in fp32. No counterpart in the reference, whose fp16 baseline is cuBLAS through
+ * F.linear (bench/e2e.py:84-147). */
+int lowbit_f16_linear_fused(const void* x, const void* w, void* y, int64_t N, int64_t K, int epilogue,
+                            const void* aux, const void* norm_weight, float eps, void* stream);
+
+/* lowbit_w4_qkv_rope over an fp16 q|k|v weight [N, K] in the same RoPE-permuted row order: the fp16 comparator of the
+ * fused decode's first projection. No counterpart in the reference. */
+int lowbit_f16_qkv_rope(const void* x, const void* w, int64_t N, int64_t K, const void* bias, const void* norm_weight,
+                        float eps, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
+                        void* v_cache, int64_t Hq, int64_t Hkv, int64_t L, void* stream);
+
 /* The RoPE factors of a step (no counterpart in the reference; the angles of lowbit_rope_kv evaluated once per step
  * instead of once per head and layer): table [M][64] of fp16 pairs (cos, sin) of positions[m] * inv_freq[i] (fp32
  * angle, cos and sin in fp32 rounded to fp16, as lowbit_rope_kv computes them). */

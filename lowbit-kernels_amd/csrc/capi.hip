@@ -397,6 +397,53 @@ int lowbit_w4_qkv_rope(const void* x, const void* w, const void* s, int64_t N, i
   return hip_status(gemv_mfma_layout_launch(a, 0), "w4_qkv_rope");
 }
 
+// the fp16-weight GEMV (the W4A16 decode's comparator): one row, K % 128 == 0, x and its norm staged in LDS
+int check_f16_fused(const void* x, const void* w, const void* y, int64_t N, int64_t K, const void* norm_weight) {
+  if (!x || !w || !y) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (N < 1 || !fits_int(N) || K < 128 || K % 128 || K > 16384)
+    return fail(LOWBIT_ERR_SHAPE, "the fp16 fused GEMV takes K a multiple of 128, at most 16384");
+  if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned");
+  if (norm_weight && !aligned16(norm_weight)) return fail(LOWBIT_ERR_ALIGN, "the norm weight must be 16-byte aligned");
+  return LOWBIT_OK;
+}
+
+int lowbit_f16_linear_fused(const void* x, const void* w, void* y, int64_t N, int64_t K, int epilogue,
+                            const void* aux, const void* norm_weight, float eps, void* stream) {
+  if (int rc = check_f16_fused(x, w, y, N, K, norm_weight)) return rc;
+  if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
+  if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
+    return fail(LOWBIT_ERR_ARG, "the bias and residual epilogues need aux");
+  if (epilogue == LOWBIT_EPI_SILU_MUL && (N % 16 || (reinterpret_cast<uintptr_t>(y) & 7)))
+    return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(x), static_cast<f16*>(y),
+             1, (int)N, (int)K, (int)K, static_cast<hipStream_t>(stream)};
+  a.epi.mode = epilogue;
+  a.epi.aux = static_cast<const f16*>(aux);
+  a.norm_w = static_cast<const f16*>(norm_weight);
+  a.eps = eps;
+  return hip_status(gemv_f16w_launch(a), "f16_linear_fused");
+}
+
+int lowbit_f16_qkv_rope(const void* x, const void* w, int64_t N, int64_t K, const void* bias, const void* norm_weight,
+                        float eps, const int64_t* positions, const float* inv_freq, void* q_out, void* k_cache,
+                        void* v_cache, int64_t Hq, int64_t Hkv, int64_t L, void* stream) {
+  if (int rc = check_f16_fused(x, w, q_out, N, K, norm_weight)) return rc;
+  if (!bias || !positions || !inv_freq || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || N != (Hq + 2 * Hkv) * 128 || !fits_int(L * 128 * Hkv))
+    return fail(LOWBIT_ERR_SHAPE, "qkv_rope: N must be (Hq + 2 Hkv) * 128 with Hkv dividing Hq, L positive");
+  if (int rc = check_device()) return rc;
+  GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(x), static_cast<f16*>(q_out),
+             1, (int)N, (int)K, (int)K, static_cast<hipStream_t>(stream)};
+  a.epi.mode = kEpiRopeQKV;
+  a.epi.aux = static_cast<const f16*>(bias);
+  a.epi.rope = RopeArgs{positions, inv_freq, nullptr, static_cast<f16*>(q_out), static_cast<f16*>(k_cache),
+                        static_cast<f16*>(v_cache), (int)Hq, (int)Hkv, (int)L};
+  a.norm_w = static_cast<const f16*>(norm_weight);
+  a.eps = eps;
+  return hip_status(gemv_f16w_launch(a), "f16_qkv_rope");
+}
+
 int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* table, int64_t M, void* stream) {
   if (!positions || !inv_freq || !table) return fail(LOWBIT_ERR_ARG, "null pointer argument");
   if (M < 1 || !fits_int(M * 64)) return fail(LOWBIT_ERR_SHAPE, "rope_table: M must be positive");

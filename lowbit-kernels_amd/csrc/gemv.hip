@@ -59,7 +59,12 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 // stay in flight through the decode at no register cost, where a register ring can refill a slot only after its
 // registers are decoded. x, the scales and the norm weights also arrive by direct-to-LDS loads, so the compiler issues
 // no vector-memory load before the main loop and every wait on the ring is counted by hand (see dma16).
-template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1, int LR = 0>
+//
+// kF16 (M = 1, R = 1, register ring, x in LDS): the same kernel over an fp16 weight [N, K] in row-major order, the
+// comparator the W4A16 decode is measured against (same tiles, waves, tile splits, prologue, reduction and epilogues;
+// only the weight bytes differ). A wave-load is then 16 rows x 32 k (64 contiguous bytes per row): lane (r, q) takes
+// k = 32 p + 8 q .. + 7 of row r for sub-load p, 4 dot2 against x; no scales, no zero sums.
+template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1, int LR = 0, bool kF16 = false>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
@@ -68,6 +73,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
                                                                            const f16* __restrict__ norm_w, float eps) {
   static_assert(CS == 1 || (R == 1 && (CS == 2 || CS == 4)), "a tile splits over 2 or 4 workgroups, one tile each");
   static_assert(LR == 0 || (M == 1 && R == 1 && kLdsX), "the LDS ring serves the one-row, one-tile GEMV");
+  static_assert(!kF16 || (M == 1 && R == 1 && LR == 0 && kLdsX), "the fp16-weight mode serves the one-row GEMV");
   constexpr int RS = 16 / CS;                               // rows of a tile one workgroup owns
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   constexpr int kScaleLoads = 4;                            // scales per thread requested before the ring
@@ -83,8 +89,9 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int q = lane & 3, rl = (lane >> 2) & (RS - 1), cs = lane / (4 * RS);   // cs: chunk within a wave-load
   const int sub = CS == 1 ? 0 : (int)blockIdx.x % CS;      // which 16 / CS rows of the tile
   const int r = RS * sub + rl;                              // this lane's row within its 16-row tile
-  const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
-  const size_t tile_bytes = (size_t)8 * K;                 // 16 rows x K/2 bytes
+  // KC: wave-loads per 16-row tile (int4: 128-k chunks; fp16: 32-k pieces)
+  const int ntiles = (N + 15) >> 4, KC = kF16 ? K >> 5 : K >> 7, KG = K / G, cpg = G >> 7;
+  const size_t tile_bytes = kF16 ? (size_t)32 * K : (size_t)8 * K;   // 16 rows x K/2 bytes (fp16: 16 rows x 2K)
   const int t0 = (CS == 1 ? (int)blockIdx.x : (int)blockIdx.x / CS) * R;
   // rows of this workgroup (none for the second half or quarters of a tile cut short by N: such a workgroup reads
   // only zeros and stores nothing). The clamp is computed per lane (v_med3); readfirstlane keeps the scale buffer
@@ -98,7 +105,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   f16* lds_s = reinterpret_cast<f16*>(smem + (LR ? RL.s : kLdsX ? (size_t)M * K * 2 + (size_t)M * (K / 32) * 8 : 0));
 
   // 1. x and scale requests
-  const int nb = M * (K / 32), ns = nrows * KG;
+  const int nb = M * (K / 32), ns = kF16 ? 0 : nrows * KG;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(ns * 2));
   u32x4 xst[XB][4], wst[XB][4];
@@ -142,9 +149,15 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     const int t = min(t0 + i, ntiles - 1);
     const int rows = t0 + i < ntiles ? min(16, N - 16 * t) : 0;
     const bool live = r < rows;
-    wr[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
-    woff[i] = live ? 64 * r + 16 * q + cs * rows * 64 : kOutOfRange;
-    wstep[i] = live ? CS * rows * 64 : 0;                  // bytes from one wave-load's chunks to the next
+    if constexpr (kF16) {                                  // row r's 64 bytes of sub-load p at 64 p
+      wr[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * K * 2));
+      woff[i] = live ? 2 * K * r + 16 * q + 64 * cs : kOutOfRange;
+      wstep[i] = live ? 64 * CS : 0;
+    } else {
+      wr[i] = make_rsrc(w + t * tile_bytes, (uint32_t)(rows * (K / 2)));
+      woff[i] = live ? 64 * r + 16 * q + cs * rows * 64 : kOutOfRange;
+      wstep[i] = live ? CS * rows * 64 : 0;                // bytes from one wave-load's chunks to the next
+    }
     srow[i] = live ? (16 * i + rl) * KG : 0;               // this lane's row in the staged scales
   }
   u32x4 ring[LR ? 1 : D][R];
@@ -184,13 +197,16 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (write_x) reinterpret_cast<u32x4*>(lds_x)[4 * b + j] = v[j];
+      if constexpr (kF16) continue;                         // fp16 weights: no offset to remove
       lo = dot2(z8lo, as_f16x2(v[j][0]), lo);
       hi = dot2(z8hi, as_f16x2(v[j][1]), hi);
       lo = dot2(z8lo, as_f16x2(v[j][2]), lo);
       hi = dot2(z8hi, as_f16x2(v[j][3]), hi);
     }
-    lds_xs[2 * b] = lo;
-    lds_xs[2 * b + 1] = hi;
+    if constexpr (!kF16) {
+      lds_xs[2 * b] = lo;
+      lds_xs[2 * b + 1] = hi;
+    }
   };
   if (LR > 0 && norm) {                                    // x and the norm weights from LDS into registers
 #pragma unroll
@@ -296,6 +312,13 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int nj = (KC / CS - wave + nwaves - 1) / nwaves;
   const uint32_t gmagic = cpg == 1 ? 0u : (uint32_t)(0xFFFFFFFFu / (uint32_t)cpg) + 1u;   // c / cpg == mulhi(c, gmagic)
   auto consume = [&](const u32x4 (&slot)[R], int cw) {
+    if constexpr (kF16) {                                   // sub-load p: k = 32 p + 8 q .. + 7 of the lane's row
+      const int p = CS * cw + cs;
+      const u32x4 xv = reinterpret_cast<const u32x4*>(lds_x + 32 * p + 8 * q)[0];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[0][0] = dot2(as_f16x2(slot[0][e]), as_f16x2(xv[e]), acc[0][0]);
+      return;
+    }
     const int c = CS * cw + cs;                             // this lane's chunk
     const int g = cpg == 1 ? c : (int)__umulhi((uint32_t)c, gmagic);
     u32x4 xv[M][4];
@@ -554,6 +577,16 @@ hipError_t dispatch_lds_ring(const GemvArgs& a, int waves, int LR) {
   }
 }
 
+// M = 1 over an fp16 weight (row-major [N, K]): the kF16 instances, epilogue and norm code compiled in
+template <int CS>
+hipError_t launch_f16w(const GemvArgs& a, int waves) {
+  const int ntiles = (a.N + 15) / 16;
+  dim3 grid(CS == 1 ? ntiles : ntiles * CS), block(64 * waves);
+  const size_t bytes = std::max<size_t>((size_t)a.K * 2, (size_t)waves * 16 * 4);
+  return launch(gemv_mfma_layout<1, 1, 4, true, true, CS, 0, true>, grid, block, bytes, a.stream, a.x, a.w, a.s, a.y,
+                a.N, a.K, a.K, a.epi, a.norm_w, a.eps);
+}
+
 template <int M, int R, int D, int CS = 1>
 hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
@@ -620,7 +653,7 @@ hipError_t dispatch_rowmajor(const GemvArgs& a, int R, bool v3) {
 
 }  // namespace
 
-GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok) {
+GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok, bool lds_ring_ok) {
   GemvPlan p;
   const int ntiles = (N + 15) / 16, KC = K / 128;
   const GemvOverride o = gemv_override();
@@ -654,11 +687,20 @@ GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_
   p.D = ((o.ring == 4 || o.ring == 8) && M <= 2) ? o.ring : 4;
   p.waves = std::min(waves, gemv_max_threads(M, p.R, p.D) / 64);
   // the weight ring in LDS: M = 1, one tile per wave, when the workgroup's LDS fits a CU and the scale tensor is a
-  // whole number of 16-byte pieces (its last piece is loaded whole)
-  if (M == 1 && p.R == 1 && o.lds_ring > 0 && (int64_t)N * (K / 128) % 8 == 0) {
-    p.LR = o.lds_ring;
-    while (p.LR > 4 && gemv_ring_lds(K, K / 128, 16 / p.CS, p.waves, p.LR, true).total > kLdsPerCu) p.LR -= 4;
-    if (gemv_ring_lds(K, K / 128, 16 / p.CS, p.waves, p.LR, true).total > kLdsPerCu) p.LR = 0;
+  // whole number of 16-byte pieces (its last piece is loaded whole). Automatic on long rows (at least 128 wave-loads
+  // per workgroup): 4 slots and 8 waves (MI355X graph sweep, cold weights: 18944 x 3584 8.10 us against 8.52 for
+  // the best register-ring shape, 16 waves; on every shorter-K decode shape the register ring is level or faster,
+  // e.g. 11008 x 2048 4.47 against 5.09, 2048 x 11008 4.66 against 5.00)
+  const bool auto_lds = lds_ring_ok && o.lds_ring == 0 && o.waves == 0 && p.CS == 1 && KC / p.CS >= 128;
+  if (M == 1 && p.R == 1 && lds_ring_ok && (o.lds_ring > 0 || auto_lds) && (int64_t)N * (K / 128) % 8 == 0) {
+    const int waves = auto_lds ? 8 : p.waves;
+    const bool norm = K <= 16384;                           // room for the fused norm's weights where it may run
+    int lr = o.lds_ring > 0 ? o.lds_ring : 4;
+    while (lr > 4 && gemv_ring_lds(K, K / 128, 16 / p.CS, waves, lr, norm).total > kLdsPerCu) lr -= 4;
+    if (gemv_ring_lds(K, K / 128, 16 / p.CS, waves, lr, norm).total <= kLdsPerCu) {
+      p.LR = lr;
+      p.waves = waves;
+    }
   }
   return p;
 }
@@ -689,6 +731,20 @@ hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
     case 7: return dispatch_mfma_layout<7>(a, p.R, p.waves, p.D, p.CS);
     default: return dispatch_mfma_layout<8>(a, p.R, p.waves, p.D, p.CS);
   }
+}
+
+hipError_t gemv_f16w_launch(const GemvArgs& a) {
+  // the int4 GEMV's plan with K counted in 32-k wave-loads (4 per 128-k chunk): the same waves and tile splits per
+  // wave-load
+  const bool row_split_ok = a.epi.mode != kEpiSiluMul && a.epi.mode != kEpiRopeQKV;
+  GemvPlan p = plan_gemv_mfma_layout(1, a.N, 4 * a.K, 1, row_split_ok, false);
+  if (a.norm_w) {
+    const int need = (a.K / 32 + 127) / 128;
+    while (p.waves < need) p.waves *= 2;
+  }
+  if (p.CS == 2) return launch_f16w<2>(a, p.waves);
+  if (p.CS == 4) return launch_f16w<4>(a, p.waves);
+  return launch_f16w<1>(a, p.waves);
 }
 
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3) {

@@ -200,12 +200,15 @@ struct ClipGrid {
   float a[kMaxClip];
 };
 
-GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok = true);
+GemvPlan plan_gemv_mfma_layout(int M, int N, int K, int rows_per_wave, bool row_split_ok = true,
+                               bool lds_ring_ok = true);
 GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_bytes);
 int pick_rows_rowmajor(int N, int M);
 
 hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave);
 hipError_t gemv_rowmajor_launch(const GemvArgs& a, int rows_per_wave, bool v3);
+// the M = 1 GEMV over an fp16 weight [N, K] (a.w, row-major; a.s unused), with the same epilogues and norm
+hipError_t gemv_f16w_launch(const GemvArgs& a);
 hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes);
 hipError_t zero_words_launch(void* p, int n, hipStream_t stream);
 // prefill variants that compile without register spills (hipcc -O3, gfx950): an 8-wave workgroup has 256 registers

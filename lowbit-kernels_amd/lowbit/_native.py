@@ -51,6 +51,9 @@ SIGNATURES = {
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "lowbit_f16_linear_fused": ([_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp, ctypes.c_float, _vp], _int),
+    "lowbit_f16_qkv_rope": ([_vp, _vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                             _i64, _vp], _int),
     "lowbit_hbm_read": ([_vp, _i64, _vp, _i64, _vp], _int),
     "lowbit_hbm_copy": ([_vp, _vp, _i64, _i64, _vp], _int),
     "lowbit_host_quantize": ([_vp, _vp, _vp, _i64, _i64, _i64], _int),
@@ -492,6 +495,50 @@ class NativeExt:
             check(self.lib.lowbit_f16_gemv(ptr(x), ptr(w), ptr(y), x.shape[0], w.shape[0], x.shape[1],
                                            _stream(x.device)))
         return y
+
+    def _check_f16_weight(self, x, w):
+        import torch
+        if not (x.is_cuda and w.is_cuda and x.device == w.device):
+            raise RuntimeError("x and w must be on the same GPU")
+        if x.dtype != torch.float16 or w.dtype != torch.float16 or not (x.is_contiguous() and w.is_contiguous()):
+            raise RuntimeError("x and w must be contiguous float16")
+        if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1] or x.shape[0] != 1:
+            raise RuntimeError("x [1, K] and w [N, K]")
+
+    def f16_linear_fused(self, x, w, epilogue, aux=None, out=None, norm=None):
+        """One row x [1, K] times an fp16 weight W [N, K]^T with the epilogue fused into the store (the W4A16 fused
+        GEMV's comparator: same kernel structure and epilogues, fp16 weight bytes); returns y ([1, N], or [1, N / 2]
+        for EPI_SILU_MUL). norm = (weight, eps): project RMSNorm(x) * weight instead of x."""
+        import torch
+        self._check_f16_weight(x, w)
+        n = w.shape[0]
+        cols = n // 2 if epilogue == EPI_SILU_MUL else n
+        y = out if out is not None else torch.empty((1, cols), dtype=torch.float16, device=x.device)
+        _need(y, "out", torch.float16, (1, cols), x.device)
+        _check_epilogue(epilogue, aux, 1, n, x.device)
+        _check_norm(norm, x.shape[1], x.device)
+        nw, eps = norm if norm is not None else (None, 0.0)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_f16_linear_fused(ptr(x), ptr(w), ptr(y), n, x.shape[1], int(epilogue),
+                                                   ptr(aux) if aux is not None else None,
+                                                   ptr(nw) if nw is not None else None, float(eps), _stream(x.device)))
+        return y
+
+    def f16_qkv_rope(self, x, w, bias, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, norm=None):
+        """w4_qkv_rope over an fp16 q|k|v weight in the same RoPE-permuted row order."""
+        import torch
+        self._check_f16_weight(x, w)
+        if w.shape[0] != (hq + 2 * hkv) * 128:
+            raise RuntimeError("the q|k|v weight must have (Hq + 2 Hkv) * 128 rows")
+        _need(bias, "bias", torch.float16, (w.shape[0],), x.device)
+        _check_norm(norm, x.shape[1], x.device)
+        self._check_rope(1, positions, inv_freq, q_out, k_cache, v_cache, hq, hkv, x.device)
+        nw, eps = norm if norm is not None else (None, 0.0)
+        with _DeviceGuard(x.device):
+            check(self.lib.lowbit_f16_qkv_rope(ptr(x), ptr(w), w.shape[0], x.shape[1], ptr(bias),
+                                               ptr(nw) if nw is not None else None, float(eps), ptr(positions),
+                                               ptr(inv_freq), ptr(q_out), ptr(k_cache), ptr(v_cache), hq, hkv,
+                                               k_cache.shape[1], _stream(x.device)))
 
     # ---- bandwidth probes (lowbit_hbm_read, lowbit_hbm_copy) ----
     def hbm_read(self, buf, sink, blocks):

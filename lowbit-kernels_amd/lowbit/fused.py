@@ -74,6 +74,19 @@ class _F16:
         return _torch_epilogue(x, self.w, epilogue, aux, out)
 
 
+class _F16GEMV:
+    """A merged fp16 projection through the library's fp16-weight GEMV for one row (lowbit_f16_linear_fused: the W4A16
+    GEMV's structure, epilogues and fused input norm over fp16 weight bytes), hipBLASLt through torch for more rows."""
+
+    def __init__(self, weight, bias=None):
+        self.w, self.bias = weight, bias
+
+    def __call__(self, x, epilogue, aux=None, out=None, norm=None):
+        if x.shape[0] == 1 and self.w.shape[1] <= 16384:
+            return ops.ext().f16_linear_fused(x, self.w, epilogue, aux, out, norm)
+        return _torch_epilogue(x, self.w, epilogue, aux, out)
+
+
 def _torch_epilogue(x, w, epilogue, aux, out, round_first=False):
     """The epilogues through torch. round_first: round the product to fp16, then add the bias or residual in fp16
     (the int4 kernels' rounding, so a W4A16 layer rounds alike on every route); otherwise fold the addend into addmm
@@ -103,7 +116,9 @@ class FusedQwen2:
 
     build(model, max_len, quant, group, clip_grid): quant = "int4" quantizes every projection with the GPU quantizer
     (the same bits as lowbit.model.quantize_layers) and keeps only the packed weights; quant = "fp16" keeps fp16
-    copies of the merged weights. forward(tokens [M], positions [M]) -> logits [M, vocab]; the KV cache rows at
+    copies of the merged weights (hipBLASLt projections); quant = "fp16_gemv" keeps them too, in the int4 variant's
+    row order, and runs one-token steps through the library's fp16-weight GEMV with the int4 variant's fusions (the
+    same launches, only the weight bytes differ). forward(tokens [M], positions [M]) -> logits [M, vocab]; the KV cache rows at
     `positions` are written, rows 0..position are attended.
     """
 
@@ -125,7 +140,7 @@ class FusedQwen2:
             att, mlp = layer.self_attn, layer.mlp
             qkv_w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).detach()
             qkv_b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).detach().half().contiguous()
-            if quant == "int4":                               # rows in the fused RoPE's order (rope_permutation)
+            if quant in ("int4", "fp16_gemv"):               # rows in the fused RoPE's order (rope_permutation)
                 perm = rope_permutation(self.hq + 2 * self.hkv, self.head_dim).to(qkv_w.device)
                 qkv_w, qkv_b = qkv_w[perm], qkv_b[perm].contiguous()
             gu_w = interleave_gate_up(mlp.gate_proj.weight.detach(), mlp.up_proj.weight.detach())
@@ -137,8 +152,10 @@ class FusedQwen2:
                     proj[name] = _W4(packed, scales, group)
             elif quant == "fp16":
                 proj = {name: _F16(w.half().contiguous()) for name, w in ws.items()}
+            elif quant == "fp16_gemv":
+                proj = {name: _F16GEMV(w.half().contiguous()) for name, w in ws.items()}
             else:
-                raise ValueError("quant is 'int4' or 'fp16'")
+                raise ValueError("quant is 'int4', 'fp16' or 'fp16_gemv'")
             proj["qkv"].bias = qkv_b
             self.layers.append({"in_norm": layer.input_layernorm.weight.detach(),
                                 "post_norm": layer.post_attention_layernorm.weight.detach(), **proj})
@@ -167,7 +184,7 @@ class FusedQwen2:
         xn = torch.empty_like(h)
         q = torch.empty(m, self.hq, self.head_dim, dtype=torch.float16, device=h.device)
         attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
-        fuse = m == 1 and self.quant == "int4" and self.hidden <= 16384
+        fuse = m == 1 and self.quant in ("int4", "fp16_gemv") and self.hidden <= 16384
         # more rows: the int4 GEMM that lay["qkv"] would pick (the MFMA GEMM up to 64 rows, the prefill GEMM where
         # prefill_path sends them) takes the RoPE epilogue too, its cos and sin from one table per step;
         # dequantize + BLAS keeps the separate rope_kv
@@ -175,7 +192,10 @@ class FusedQwen2:
                      (m <= 64 or ops.prefill_path(m, self.layers[0]["qkv"].wq)) if self.layers else False)
         table = ext.rope_table(positions, self.inv_freq) if rope_rows else None
         for i, lay in enumerate(self.layers):
-            if fuse:                                          # RMSNorm in the prologue, RoPE + cache write in the store
+            if fuse and self.quant == "fp16_gemv":
+                ext.f16_qkv_rope(h, lay["qkv"].w, lay["qkv"].bias, positions, self.inv_freq, q, self.k_cache[i],
+                                 self.v_cache[i], self.hq, self.hkv, norm=(lay["in_norm"], self.eps))
+            elif fuse:                                        # RMSNorm in the prologue, RoPE + cache write in the store
                 wq = lay["qkv"].wq
                 ext.w4_qkv_rope(h, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, self.inv_freq, q,
                                 self.k_cache[i], self.v_cache[i], self.hq, self.hkv, norm=(lay["in_norm"], self.eps))
@@ -188,7 +208,7 @@ class FusedQwen2:
                 ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
                 qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
                 ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv,
-                            permuted=self.quant == "int4")
+                            permuted=self.quant in ("int4", "fp16_gemv"))
             ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
                           self.scale)
             lay["o"](attn, EPI_RESIDUAL, h, out=h)

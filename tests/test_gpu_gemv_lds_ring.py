@@ -53,6 +53,22 @@ def test_lds_ring_equals_register_ring(cuda, reset, k, n):
                 assert torch.equal(ops.gemv(x, wq, 6), got)         # the same bits on every call
 
 
+@pytest.mark.parametrize("k,n", [(18944, 3584), (16384, 4096), (18944, 2060)])
+def test_automatic_plan_on_long_rows(cuda, reset, k, n):
+    """Rows of at least 128 chunks on layers of more than 128 tiles (whole tiles per workgroup) take the LDS ring
+    automatically (4 slots, 8 waves): the register ring forced to 8 waves gives the same bits, and both are within the
+    bound of the fp64 product (2060 rows: a last tile of 12)."""
+    wq, ref_w, *_, gen = make_weight(k, n, 9 * k + n, layouts=("mma",), sd=0.02)
+    x = torch.randn(1, k, generator=gen).half().cuda()
+    ref = x.double() @ ref_w.T
+    auto = ops.gemv(x, wq, 6)
+    set_shape(8, 1)
+    set_ring(-1)
+    want = ops.gemv(x, wq, 6)
+    assert torch.equal(auto, want), (k, n)
+    assert rel(auto, ref) <= bound(x, ref_w, ref), (k, n)
+
+
 @pytest.mark.parametrize("k,n", [(2048, 2048), (1536, 208), (8960, 1536)])
 def test_lds_ring_epilogues_and_norm(cuda, reset, k, n):
     ext = ops.ext()
