@@ -44,8 +44,8 @@ CLIP_GRID = tuple(round(1.0 - 0.025 * i, 3) for i in range(11))       # referenc
 HBM_PEAK_GBPS = 8000.0
 # HBM bytes per GEMV launch of this workload, measured: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
 # `bench.py --pmc-workload` (20 eager steps), each scaled by what the counter reads for a 1 GiB elementwise copy in the
-# same run (FETCH x2.0, WRITE x1.0); 1.032x the algorithmic bytes. Re-measure when the kernel changes.
-TRAFFIC_PER_LAUNCH = 4723463
+# same run (FETCH x2.0, WRITE x1.0); 1.034x the algorithmic bytes. Re-measure when the kernel changes.
+TRAFFIC_PER_LAUNCH = 4730115
 MODELS = {"1.5b": (1536, 8960), "3b": (2048, 11008)}                   # hidden, intermediate; 2 KV heads x 128
 
 
@@ -86,7 +86,7 @@ def parse():
                          "give the spread")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter workload: a 1 GiB elementwise copy (calibration), then eager steps, nothing else")
-    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "ldsring", "tiles", "tilewaves", "splits"],
+    ap.add_argument("--sweep", choices=["skinny", "prefill", "gemv", "ldsring", "order", "tiles", "tilewaves", "splits"],
                     default=None,
                     help="skinny: M=1..64 per path; prefill: M>64; gemv: the M=1 GEMV's tile split x waves; "
                          "ldsring: the M=1 GEMV's weight ring in registers vs in LDS; "
@@ -865,6 +865,36 @@ def sweep_ldsring(a):
         pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
 
 
+ORDER_SHAPES = [(11008, 2048), (8960, 1536), (18944, 3584), (2048, 2048), (3584, 3584), (2048, 2560), (1536, 2048),
+                (3584, 4608)]
+
+
+def sweep_order(a):
+    """MFMA GEMM (v5) with a K split, M = 2..64: graph-timed us per call with the row groups fastest in the
+    workgroup order (lowbit_set_gemm_order 1) and with the splits fastest (2), over >= 1 GiB of cold copies."""
+    import torch
+    from lowbit import _native, ops
+    torch.cuda.set_device(0)
+    lib = _native.lib()
+    rows = []
+    for k, n in ORDER_SHAPES:
+        cl = cloned_copies(torch, ops, k, n)
+        r = {"K": k, "N": n, "us": {}}
+        for m in SKINNY_BLOCK_M:
+            x = torch.randn(m, k, device="cuda").half()
+            for order in (1, 2):
+                _native.check(lib.lowbit_set_gemm_order(order))
+                r["us"][f"{m}:{order}"] = round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5),
+                                                              max(400, len(cl))), 2)
+        _native.check(lib.lowbit_set_gemm_order(0))
+        rows.append(r)
+        print(json.dumps(r), flush=True)
+        del cl
+        torch.cuda.empty_cache()
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(rows, indent=1))
+
+
 def sweep_tiles(a):
     """MFMA GEMM (v5) per decode shape and M in 2..64: graph-timed us per call of the row-group kernel (automatic
     shape), of one tile per workgroup with 2, 4 and 8 waves, and of the automatic choice (lowbit_set_gemm_kernel)."""
@@ -1272,6 +1302,8 @@ def main():
         sweep_gemv(a)
     elif a.sweep == "ldsring":
         sweep_ldsring(a)
+    elif a.sweep == "order":
+        sweep_order(a)
     elif a.sweep == "tiles":
         sweep_tiles(a)
     elif a.sweep == "tilewaves":

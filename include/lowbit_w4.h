@@ -73,6 +73,12 @@ int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits);
  * reference. */
 int lowbit_set_gemv_lds_ring(int slots);
 
+/* Process-wide choice of the MFMA GEMM's workgroup order when K is split across workgroups, for tuning sweeps and
+ * tests: 0 = automatic; 1 = row groups fastest; 2 = splits fastest (the workgroups of one split, which read the same
+ * slice of x, share an XCD). The split partials are added in split order either way, so the results are identical
+ * bit for bit. Affects later launches only. No counterpart in the reference. */
+int lowbit_set_gemm_order(int order);
+
 /* Process-wide choice of the MFMA GEMM's structure (lowbit_w4_gemm_mfma, lowbit_w4_linear_fused for M >= 2), for
  * tuning sweeps and tests: 0 = automatic; 1 = row groups of 64 or 128 weight rows sharing staged activations, K split
  * across workgroups on narrow layers; 2 = one 16-row tile per workgroup, its waves splitting K (M <= 32 only; larger M

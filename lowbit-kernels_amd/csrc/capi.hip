@@ -35,7 +35,7 @@ int check_device() {
 }
 
 std::atomic<int> g_override_waves{0}, g_override_ring{0}, g_override_splits{0}, g_override_gemm{0},
-    g_override_tile_waves{0}, g_override_lds_ring{0};
+    g_override_tile_waves{0}, g_override_lds_ring{0}, g_override_gemm_order{0};
 
 int hip_status(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(LOWBIT_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
@@ -121,6 +121,7 @@ GemvOverride gemv_override() {
   o.gemm_kernel = g_override_gemm.load(std::memory_order_relaxed);
   o.tile_waves = g_override_tile_waves.load(std::memory_order_relaxed);
   o.lds_ring = g_override_lds_ring.load(std::memory_order_relaxed);
+  o.gemm_order = g_override_gemm_order.load(std::memory_order_relaxed);
   return o;
 }
 
@@ -202,6 +203,12 @@ int lowbit_set_gemv_lds_ring(int slots) {
   if (!(slots == 0 || slots == -1 || slots == 4 || slots == 8 || slots == 12 || slots == 16))
     return fail(LOWBIT_ERR_TUNING, "slots is 0 (auto), -1 (ring in registers), 4, 8, 12 or 16");
   g_override_lds_ring.store(slots, std::memory_order_relaxed);
+  return ok();
+}
+
+int lowbit_set_gemm_order(int order) {
+  if (order < 0 || order > 2) return fail(LOWBIT_ERR_TUNING, "order is 0 (auto), 1 (row groups fastest) or 2 (splits fastest)");
+  g_override_gemm_order.store(order, std::memory_order_relaxed);
   return ok();
 }
 

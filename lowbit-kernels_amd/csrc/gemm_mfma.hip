@@ -69,7 +69,11 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   const int gt = tid - kGroupThreads * kg;                  // thread index inside the K-group
   const int r = lane & 15, q = lane >> 4;
   const int ntiles = (N + 15) >> 4, KC = K >> 7, KG = K / G, cpg = G >> 7;
-  const int grp = blockIdx.x, split = blockIdx.y;
+  // a two-dimensional grid numbers row groups fastest (the S splits of a row group on one XCD when the row groups
+  // number a multiple of 8); a one-dimensional one numbers the splits fastest (workgroup i on XCD i % 8, so the
+  // workgroups of a split, which read the same slice of x, share an XCD and its L2)
+  const bool flat = gridDim.y == 1;
+  const int grp = flat ? (int)blockIdx.x / S : (int)blockIdx.x, split = flat ? (int)blockIdx.x % S : (int)blockIdx.y;
   const int n0 = 16 * T * grp;
   const int cb = (int)((int64_t)KC * split / S), ce = (int)((int64_t)KC * (split + 1) / S);
   const int nsteps = (ce - cb + KS - 1) / KS;               // K-group kg takes chunks cb + kg + KS j
@@ -502,8 +506,9 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
       if (attr[0] != hipSuccess) return attr[0];
       if (attr[1] != hipSuccess) return attr[1];
     }
-    return launch(kern, dim3(groups, p.S), dim3(64 * TW * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K,
-                  a.G, p.S, ctr, part, a.epi);
+    const dim3 grid = p.XO ? dim3(groups * p.S) : dim3(groups, p.S);
+    return launch(kern, grid, dim3(64 * TW * KS), shmem, a.stream, a.x, a.w, a.s, a.y, a.M, a.N, a.K, a.G, p.S, ctr,
+                  part, a.epi);
   }
 }
 
@@ -696,6 +701,7 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   }
   p.waves = KW * ks;
   p.S = std::max(S, 1);
+  p.XO = p.S > 1 && o.gemm_order == 2 ? 1 : 0;
   // one arrival counter per row group of the final shape (R may have dropped to 1 above)
   if (p.S > 1 && (ntiles + KW * p.R - 1) / (KW * p.R) > (int)(kCounterBytes / 4)) p.S = 1;
   return p;

@@ -105,6 +105,7 @@ struct GemvPlan {
   int TW = 0;       // MFMA GEMM: waves of the one-tile-per-workgroup kernel (0: the row-group kernel)
   int KW = 4;       // MFMA GEMM row groups: tile-waves per K-group (4, or 5, 6, 8 with one tile per wave)
   int LR = 0;       // M = 1 GEMV: weight ring slots per wave held in LDS (direct-to-LDS loads); 0 = ring in registers
+  int XO = 0;       // MFMA GEMM with a K split: 0 row groups fastest in the workgroup order, 1 splits fastest
 };
 
 // launch shape of the prefill GEMM (M > 64)
@@ -127,6 +128,7 @@ struct GemvOverride {
   int gemm_kernel = 0;  // MFMA GEMM structure: 0 automatic, 1 row groups (K split across workgroups), 2 one tile each
   int tile_waves = 0;   // MFMA GEMM row groups: tile-waves per K-group (0 automatic, 3, 4, 5, 6 or 8)
   int lds_ring = 0;     // M = 1 GEMV: 0 automatic, -1 ring in registers, 4 / 8 / 12 / 16 slots per wave in LDS
+  int gemm_order = 0;   // MFMA GEMM with a K split: 0 automatic, 1 row groups fastest, 2 splits fastest
 };
 GemvOverride gemv_override();
 

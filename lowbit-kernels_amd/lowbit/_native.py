@@ -30,6 +30,7 @@ SIGNATURES = {
     "lowbit_set_launch_override": ([_int, _int, _int], _int),
     "lowbit_set_gemm_kernel": ([_int], _int),
     "lowbit_set_gemv_lds_ring": ([_int], _int),
+    "lowbit_set_gemm_order": ([_int], _int),
     "lowbit_set_gemm_tile_waves": ([_int], _int),
     "lowbit_w4_gemv": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _int, _vp], _int),
     "lowbit_w4_gemm_mfma": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp, ctypes.c_size_t, _vp], _int),

@@ -163,3 +163,27 @@ def test_tiny_activations_keep_their_precision(cuda):
     for m in range(4):
         ym = gemm(x, wq, 2, 4, 4, ws)[m:m + 1]
         assert rel(ym, ref[m:m + 1]) <= R.REL_BOUND, m
+
+
+@pytest.mark.parametrize("k,n", [(11008, 2048), (3584, 200), (18944, 3584), (2048, 1001)])
+def test_split_order_gives_the_same_bits(cuda, k, n):
+    """The workgroup order of a K-split launch (row groups fastest, or splits fastest so that one split's workgroups
+    share an XCD) only changes where the workgroups run: the same bits at every split count and row count, the
+    counters left at zero."""
+    wq, ref_w, *_, gen = make_weight(k, n, 7 * k + n, layouts=("mma",))
+    ws = _native.workspace(torch.device("cuda", 0), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    lib = _native.lib()
+    try:
+        for m in (2, 16, 48, 64):
+            x = torch.randn(m, k, generator=gen).half().cuda()
+            for splits in (0, 2, 3, 8, 16):
+                outs = []
+                for order in (1, 2):
+                    _native.check(lib.lowbit_set_gemm_order(order))
+                    outs.append(gemm(x, wq, 1, 0, splits, ws))
+                assert torch.equal(outs[0], outs[1]), (k, n, m, splits)
+            assert rel(outs[1], x.double() @ ref_w.T) <= bound(x, ref_w, x.double() @ ref_w.T)
+    finally:
+        _native.check(lib.lowbit_set_gemm_order(0))
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(ws[:_native.WORKSPACE_COUNTER_BYTES])) == 0
