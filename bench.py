@@ -101,6 +101,8 @@ def parse():
     ap.add_argument("--chunk", type=int, default=1,
                     help="with --decode-trace: tokens fed per captured step (1 = greedy decoding)")
     ap.add_argument("--no-decode", action="store_true", help="skip the configs[4] decode block")
+    ap.add_argument("--host-cost", action="store_true",
+                    help="per-call host cost of the M=1 entry points and eager vs graph decode (3B)")
     ap.add_argument("--no-trace", action="store_true",
                     help="skip the traced run of the timed workload (roofline from graph time per launch instead)")
     ap.add_argument("--trace-child", action="store_true",
@@ -497,6 +499,94 @@ def decode_block(torch, ops):
                 "fused_int4_over_hf_fp16": {"greedy_ms_per_token": sp("fused_int4", "hf_fp16",
                                                                       "greedy_ms_per_token")}},
             "ttft_ms": {k: v["ttft_ms"] for k, v in out.items()}}
+
+
+def host_cost(a):
+    """Host cost of one M = 1 call and eager decode (reference bench/gpu_run.py:304-322, bench/e2e.py:54-69).
+    * Per call, interleaved over rounds (min of 7 rounds of 2000 back-to-back calls, wall time / calls after a
+      synchronization): the C entry point through ctypes with a preallocated output (the floor), ext().w4_gemv
+      (validation, torch.empty, launch), ops.gemv and ops.linear (routing on top), on a small and a mid-size decode
+      layer, next to the GPU time per call of the same launch in a graph: where wall > graph time the host is the
+      bound in eager mode.
+    * Eager greedy decode (every step launched op by op) of the random-init Qwen2.5-3B architecture against the
+      graph replay, for the fused layers (W4A16 and fp16 through the same GEMV) and transformers' modules (fp16 and
+      the W4Linear drop-in)."""
+    import ctypes
+    import torch
+    from lowbit import _native, decode, fused, ops, model as lbmodel
+    torch.cuda.set_device(0)
+    lib, ext = _native.lib(), ops.ext()
+    out = {"per_call_us": {}}
+    for k, n in ((1536, 256), (2048, 2048)):
+        wq = ops.W4Weight.from_float(torch.randn(n, k, device="cuda") * 0.02, GROUP, ("mma",))
+        x = torch.randn(1, k, device="cuda").half()
+        y = torch.empty(1, n, dtype=torch.half, device="cuda")
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        args = (_native.ptr(x), _native.ptr(wq.packed_mma), _native.ptr(wq.scales), _native.ptr(y), 1, n, k, GROUP, 6,
+                0, st)
+        calls = {"c_abi_ctypes": lambda: lib.lowbit_w4_gemv(*args),
+                 "ext_w4_gemv": lambda: ext.w4_gemv(x, wq.packed_mma, wq.scales, GROUP, 6),
+                 "ops_gemv": lambda: ops.gemv(x, wq, 6),
+                 "ops_linear": lambda: ops.linear(x, wq)}
+        best = {name: 1e30 for name in calls}
+        for _ in range(7):
+            for name, fn in calls.items():
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(2000):
+                    fn()
+                torch.cuda.synchronize()
+                best[name] = min(best[name], (time.perf_counter() - t0) / 2000 * 1e6)
+        r = {name: round(v, 2) for name, v in best.items()}
+        r["gpu_graph_us"] = round(graph_time_us(torch, lambda i: ops.linear(x, wq), 2000), 2)
+        out["per_call_us"][f"{k}x{n}"] = r
+        progress(f"host cost {k}x{n}: {r}")
+    cfg = DECODE_BLOCK
+    m = decode.random_model(cfg["model"], seed=0)
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    prompt = torch.randint(0, m.config.vocab_size, (1, cfg["prompt"]), generator=gen, device="cuda")
+    n_tok = 32
+    max_len = cfg["prompt"] + 2 * n_tok + 16
+
+    def run(dec):
+        res = {}
+        for mode in ("graph", "eager"):
+            first = dec.prefill(prompt).argmax(-1)
+            if mode == "graph":
+                dec.capture()
+                first = dec.prefill(prompt).argmax(-1)
+                fn = lambda: dec.greedy(first, n_tok)  # noqa: E731
+            else:
+                fn = lambda: dec.eager_greedy(first, n_tok)  # noqa: E731
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            res[f"{mode}_ms_per_token"] = round((time.perf_counter() - t0) * 1000 / (n_tok - 1), 4)
+        res["eager_over_graph"] = round(res["eager_ms_per_token"] / res["graph_ms_per_token"], 3)
+        return res
+    dec_out = {}
+    for quant in ("int4", "fp16_gemv"):
+        fq = fused.FusedQwen2(m, max_len, quant=quant, clip_grid=CLIP_GRID if quant == "int4" else None)
+        run(fused.FusedDecoder(fq, 1))                       # warm-up of both modes
+        dec_out[f"fused_{quant}"] = run(fused.FusedDecoder(fq, 1))
+        del fq
+        torch.cuda.empty_cache()
+    run(decode.GraphDecoder(m, max_len, 1))
+    dec_out["hf_fp16"] = run(decode.GraphDecoder(m, max_len, 1))
+    lbmodel.apply_int4(lbmodel.quantize_layers(m, GROUP, CLIP_GRID))
+    run(decode.GraphDecoder(m, max_len, 1))
+    dec_out["hf_w4linear"] = run(decode.GraphDecoder(m, max_len, 1))
+    out["decode_3b"] = {"tokens": n_tok, "prompt": cfg["prompt"], **dec_out,
+                        "eager_w4_over_fp16": {
+                            "fused": round(dec_out["fused_fp16_gemv"]["eager_ms_per_token"] /
+                                           dec_out["fused_int4"]["eager_ms_per_token"], 3),
+                            "transformers": round(dec_out["hf_fp16"]["eager_ms_per_token"] /
+                                                  dec_out["hf_w4linear"]["eager_ms_per_token"], 3)}}
+    out["host"] = {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+    print(json.dumps(out), flush=True)
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(out, indent=1))
 
 
 def per_shape_extra(torch, ops, peak=None):
@@ -1314,6 +1404,8 @@ def main():
         decode_trace(a)
     elif a.e2e:
         e2e(a)
+    elif a.host_cost:
+        host_cost(a)
     elif a.trace_child:
         a.no_cpu = a.no_fp16 = a.no_detail = True
         a.trace = None

@@ -140,3 +140,19 @@ class GraphDecoder:
             self.step(out[i - 1])
             out[i] = self.next_token
         return out
+
+    @torch.inference_mode()
+    def eager_greedy(self, first, n):
+        """greedy() without the graph: every step is the model's own forward, launched op by op from the host (the
+        reference's eager decode, bench/e2e.py:54-69). Needs a prefill and a cache with room for n - 1 steps."""
+        if self.chunk != 1 or self.pos + n - 1 > self.max_len:
+            raise ValueError("eager greedy decoding feeds one token per step within the cache")
+        out = torch.empty(n, dtype=torch.long, device=self.tokens.device)
+        out[0] = first
+        for i in range(1, n):
+            self.tokens.copy_(out[i - 1].view(1, 1))
+            self.positions.copy_(self.offsets + self.pos)
+            self._sync_write_position()
+            out[i] = self._forward()[-1].argmax(-1)
+            self.pos += 1
+        return out

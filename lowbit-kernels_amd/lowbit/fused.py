@@ -271,6 +271,19 @@ class FusedDecoder:
                 self.positions.add_(1)
         return self
 
+    @torch.inference_mode()
+    def eager_greedy(self, first, n):
+        """n greedy tokens after a prefill, every step launched op by op from the host (no graph)."""
+        if self.chunk != 1 or self.pos + n - 1 > self.f.max_len:
+            raise ValueError("eager greedy decoding feeds one token per step within the cache")
+        out = torch.empty(n, dtype=torch.long, device=self.tokens.device)
+        out[0] = first
+        for i in range(1, n):
+            self.positions.fill_(self.pos)
+            out[i] = self.f(out[i - 1].view(1), self.positions)[-1].argmax(-1)
+            self.pos += 1
+        return out
+
     def step(self, tokens):
         if self.pos + self.chunk > self.f.max_len:
             raise ValueError("the cache is full")

@@ -9,6 +9,10 @@ checks its decode path (bench/e2e.py:219-250):
   that model's own noise floor: the same fake-quant model fed one token per step, which changes nothing but fp16
   summation order and rounding, through 28 or 36 layers. The worst logit difference (max over 96 x 151936 logits,
   relative to their RMS) must stay within max(2e-2, 2 x the floor's), next-token (argmax) agreement at least 95%;
+* every W4Linear projection of the full model, hooked during a step (1 and 16 rows, and the prompt), against the fp64
+  product of its own input and dequantized weights within the reference's bound (3e-3 of the output RMS, or 4 x the
+  fp16 output floor or BLAS error where larger): a per-kernel check on real activations that does not compound
+  through the layers;
 * every graph replay gives the bits of the same step run eagerly;
 * greedy decoding of 32 tokens with the argmax taken inside the graph equals eager greedy decoding step by step.
 
@@ -166,6 +170,58 @@ def run_greedy(b, tag):
         ge.pos += 1
     say(f"[{tag}] W4Linear greedy: {toks[:8]} ...")
     assert toks == eager
+
+
+def run_per_projection(b, tag):
+    """Every W4Linear projection of the full model, hooked during one teacher-forced step at 1, 16 (GEMV, MFMA GEMM)
+    and the prompt's rows (prefill route): its output against the fp64 product of the same input with the same
+    dequantized weights (+ bias), within the reference's bound (max(4 x BLAS error, 4 x fp16 output floor, 3e-3) of
+    the output RMS, bench/gpu_run.py:229-245).
+    Unlike the logits, this does not compound through the layers, so a kernel regression on any one projection
+    shape trips it."""
+    from lowbit import ops
+    seen = []
+
+    def hook(mod, inp, out):
+        x = inp[0].reshape(-1, inp[0].shape[-1])
+        w = ops.dequant(mod.wq).double()
+        ref = x.double() @ w.T
+        if mod.bias is not None:
+            ref = ref + mod.bias.double()
+        rms = ref.pow(2).mean().sqrt()
+        err = float((out.reshape(ref.shape).double() - ref).abs().max() / rms)
+        # the reference's acceptance rule: max(4 x the BLAS error on the dequantized fp16 weight, 4 x the fp16 output
+        # rounding floor, 3e-3)
+        blas = torch.nn.functional.linear(x, w.half()).double() + (mod.bias.double() if mod.bias is not None else 0)
+        lim = max(4 * float((blas - ref).abs().max() / rms), 4 * float((ref.half().double() - ref).abs().max() / rms),
+                  3e-3)
+        seen.append((x.shape[0], tuple(w.shape), err, lim))
+
+    handles = [mod.register_forward_hook(hook) for mod in b.model.modules() if isinstance(mod, lbmodel.W4Linear)]
+    try:
+        for chunk in (1, 16):
+            dec = decode.GraphDecoder(b.model, b.max_len, chunk)
+            dec.prefill(b.prompt)                           # the prompt's rows: the prefill route
+            dec.tokens.copy_(b.feed[:chunk].view(1, chunk))
+            dec.positions.copy_(dec.offsets + dec.pos)
+            with torch.inference_mode():
+                dec._forward()
+    finally:
+        for h in handles:
+            h.remove()
+    worst = max(seen, key=lambda t: t[2] / t[3])
+    say(f"[{tag}] {len(seen)} projection calls, worst {worst[2]:.2e} of RMS against its bound {worst[3]:.2e} "
+        f"(rows {worst[0]}, weight {worst[1]}); errors {min(t[2] for t in seen):.2e} .. {max(t[2] for t in seen):.2e}")
+    bad = [t for t in seen if t[2] > t[3]]
+    assert not bad, bad[:5]
+
+
+def test_qwen25_1p5b_per_projection(cuda, qwen15b):
+    run_per_projection(qwen15b, "1.5B")
+
+
+def test_qwen25_3b_per_projection(cuda, qwen3b):
+    run_per_projection(qwen3b, "3B")
 
 
 def test_qwen25_1p5b_teacher_forced(cuda, qwen15b):
