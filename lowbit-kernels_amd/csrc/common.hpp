@@ -171,6 +171,36 @@ __device__ __forceinline__ f32x4 load_partial4(__amdgpu_buffer_rsrc_t r, int off
 __device__ __forceinline__ float load_partial(__amdgpu_buffer_rsrc_t r, int offset) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, kAgentCoherent));
 }
+// The K split's fixup: the sum of the S partials of four outputs at byte offsets off(0) .. off(S - 1), added in split
+// order. The loads go out in batches of 8 before the first add: a loop that adds each partial as it loads it waits one
+// memory round trip per split (measured on MI355X: 3.0 us of a 12 us launch at S = 8). `lanes` < 4: only the first
+// `lanes` outputs exist, loaded and added one by one.
+template <typename Off>
+__device__ __forceinline__ f32x4 sum_partials4(__amdgpu_buffer_rsrc_t r, int S, int lanes, Off off) {
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    if (lanes == 4) {
+      f32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = load_partial4(r, s0 + u < S ? off(s0 + u) : kOutOfRange);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (s0 + u < S) sum += v[u];
+    } else {
+      float v[8][4];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[u][e] = load_partial(r, s0 + u < S && e < lanes ? off(s0 + u) + 4 * e : kOutOfRange);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (s0 + u < S && e < lanes) sum[e] += v[u][e];
+    }
+  }
+  return sum;
+}
 
 // ---- direct-to-LDS loads (gfx950: 16 bytes per lane) ----
 // The LDS byte address of a __shared__ object.

@@ -313,16 +313,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   if (tid == 0) __hip_atomic_store(ctr + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nrows = min(16 * T, N - n0), nq = (nrows + 3) >> 2;
   auto split_sum = [&](int m, int n) {                      // partials of rows n .. n + 3, added in split order
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    if ((N & 3) == 0) {
-      for (int sp = 0; sp < S; ++sp) sum += load_partial4(pr, poff(sp, m, n));
-    } else {
-      for (int sp = 0; sp < S; ++sp)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) sum[e] += load_partial(pr, poff(sp, m, n) + 4 * e);
-    }
-    return sum;
+    return sum_partials4(pr, S, (N & 3) == 0 ? 4 : min(4, N - n), [&](int sp) { return poff(sp, m, n); });
   };
   for (int it = tid; it < M * nq; it += kGroupThreads * KS) {
     const int m = it / nq, n = n0 + 4 * (it - m * nq);

@@ -267,16 +267,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ 
   if (tid == 0) __hip_atomic_store(ctr + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int nrows = min(kRows, N - n0), nq = (nrows + 3) >> 2, mrows = min(16 * MT, M - m0);
   auto split_sum = [&](int m, int n) {                      // partials of rows n .. n + 3, added in split order
-    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
-    if ((N & 3) == 0) {
-      for (int k = 0; k < S; ++k) sum += load_partial4(pr, poff(k, m, n));
-    } else {
-      for (int k = 0; k < S; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < N) sum[e] += load_partial(pr, poff(k, m, n) + 4 * e);
-    }
-    return sum;
+    return sum_partials4(pr, S, (N & 3) == 0 ? 4 : min(4, N - n), [&](int k) { return poff(k, m, n); });
   };
   for (int it = tid; it < mrows * nq; it += kThreads) {
     const int m = m0 + it / nq, n = n0 + 4 * (it % nq);
