@@ -1061,9 +1061,9 @@ def sweep_tilewaves(a):
 
 
 def sweep_splits(a):
-    """MFMA GEMM (v5) on the 1.5B / 3B / 7B decode projections, M in {16, 32, 48, 64}: graph-timed us per call of the
-    automatic plan, of one tile per workgroup (lowbit_set_gemm_kernel(2)) and of the row groups
-    (lowbit_set_gemm_kernel(1)) with every K split S in {1, 2, 4, 8} x K-groups ks in {1, 2, 4} forced through
+    """MFMA GEMM (v5) on the 1.5B / 3B / 7B decode projections, M in {2, 16, 32, 48, 64}: graph-timed us per call of
+    the automatic plan, of one tile per workgroup (lowbit_set_gemm_kernel(2)) and of the row groups
+    (lowbit_set_gemm_kernel(1)) with every K split S in {1, 2, 4, 8, 16} x K-groups ks in {1, 2, 4} forced through
     lowbit_set_launch_override(4 ks, 0, S), the rest automatic."""
     import torch
     from lowbit import _native, ops
@@ -1073,7 +1073,7 @@ def sweep_splits(a):
     for k, n in ((1536, 2048), (1536, 1536), (2048, 2560), (2048, 2048), (3584, 3584), (3584, 512), (2048, 256),
                  (1536, 256), (3584, 4608), (8960, 1536), (11008, 2048), (18944, 3584)):
         cl = cloned_copies(torch, ops, k, n, gib=0.5)
-        for m in (16, 32, 48, 64):
+        for m in (2, 16, 32, 48, 64):
             x = torch.randn(m, k, device="cuda").half()
             t = lambda: round(graph_time_us(torch, lambda i: ops.gemv(x, cl[i % len(cl)], 5), max(200, len(cl))), 2)
             r = {"K": k, "N": n, "M": m, "auto": t()}
@@ -1081,7 +1081,7 @@ def sweep_splits(a):
                 _native.check(lib.lowbit_set_gemm_kernel(2))
                 r["tiles"] = t()
                 _native.check(lib.lowbit_set_gemm_kernel(1))
-                for sp in (1, 2, 4, 8):
+                for sp in (1, 2, 4, 8, 16):
                     for ks in (1, 2, 4):
                         if sp * ks <= k // 128:
                             _native.check(lib.lowbit_set_launch_override(4 * ks, 0, sp))

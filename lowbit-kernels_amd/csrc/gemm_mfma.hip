@@ -618,10 +618,13 @@ int balanced_tile_waves(int ntiles, int MT) {
 
 // Launch shape from an MI355X sweep (graph-timed, cold weights, M in 2..64 on the Qwen2.5-3B/7B MLP shapes): one
 // tile per wave; K split across workgroups while the row groups times the split stay within 256 workgroups (narrow
-// N), every split keeps at least 4 chunks and K has at least 16 (1536 x 2048 at M = 48: 8.4 us unsplit against 8.9
-// split 2 ways), only for layers with fewer than 128 row groups (1536 x 8960, 140 row
-// groups, split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row groups, 4 ways; 2048 x 2048 at M = 32 7.0 us with
-// 4 ways against 8.4 with 8; 3584 x 4608, 72 row groups, 9.6 with 2 against 10.8 with 4); K-groups per workgroup until
+// N) and every split keeps at least 4 chunks, or 2 while the workgroups stay within half of 256, only for layers with
+// fewer than 128 row groups (1536 x 8960, 140 row groups, split 2 ways 19.7 us, unsplit 5.9 us; 3584 x 3584, 56 row
+// groups, 4 ways; 2048 x 2048 at M = 32 6.6-7.0 us with 4 ways against 7.1-8.4 with 8; 3584 x 4608, 72 row groups,
+// 9.6 with 2 against 10.8 with 4). The 2-chunk splits pay since the fixup requests every partial at once (`bench.py
+// --sweep splits`: 3584 x 512 at M = 16..64 8 ways 5.9-9.1 us against 6.6-10.4 with 4; 2048 x 256 at M = 32..64 8
+// ways, 6-9% faster; 1536 x 2048 and 1536 x 256 at M = 64 4 ways, 8.9 / 8.8 us against 9.6 unsplit). K-groups per
+// workgroup until
 // about kGemmTargetWaves waves run (at most 2 K-groups for 17..32 rows; up to 16 rows 4, also where the row groups
 // alone reach that many waves: 3584 x 16384, 256 row groups, M = 16, 10.3 -> 9.6 us against 2); from 33 rows K-groups
 // double only while the waves stay within kGemmMaxWavesWide (3B gate/up at M = 64 12.3 us with 2 K-groups against
@@ -653,7 +656,9 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
   if (o.splits > 0) {
     S = o.splits;
   } else if (part_bytes > 0) {
-    while (S < kMaxSplits && groups < 128 && (long)groups * S * 2 <= kGemmMaxGroups && KC >= 8 * S && KC >= 16) S *= 2;
+    while (S < kMaxSplits && groups < 128 && (long)groups * S * 2 <= kGemmMaxGroups &&
+           KC >= ((long)groups * S * 2 <= kGemmMaxGroups / 2 ? 4 : 8) * S)
+      S *= 2;
   }
   S = std::min(S, std::max(1, KC));
   while (S > 1 && (size_t)S * M * N * sizeof(float) > part_bytes) --S;
@@ -671,10 +676,13 @@ GemvPlan plan_gemm_mfma(int M, int N, int K, int row_tiles, size_t workspace_byt
     while (ks < 2 && (long)groups * S * KW * ks < kGemmTargetWaves && 2 * ks * S <= KC) ks *= 2;
   } else {
     // from 33 rows: fewer, longer K-groups (see above), and on an unsplit layer at least 4 chunks each (1536 x 2048
-    // at M = 48: 7.97 us with 2 against 8.35 with 4); but up to 4 on layers split 4 or more ways (11008 x 2048 at
-    // M = 48 13.3 us against 15.2 with 2; 2048 x 2560 8.1 against 9.1; 3584 x 3584 10.4 against 11.0)
+    // at M = 48: 7.97 us with 2 against 8.35 with 4); but up to 4 on layers split 4 or more ways (2048 x 2560 7.9 us
+    // against 8.2 with 2; 2048 x 2048 7.8 against 8.0), except, at 33-48 rows, where each split keeps 6 chunks or more
+    // (8960 x 1536 at M = 48 10.9 us with 2 against 11.8 with 4, 11008 x 2048 12.0 against 12.6, 3584 x 3584 10.0
+    // against 10.2)
     const long cap = S >= 4 ? 2L * kGemmMaxWavesWide : (long)kGemmMaxWavesWide;
-    while (ks < 4 && (long)groups * S * KW * 2 * ks <= cap && 2 * ks * S <= KC && (S > 1 || 8 * ks <= KC)) ks *= 2;
+    const int ks_max = p.MT == 3 && KC / S >= 6 ? 2 : 4;
+    while (ks < ks_max && (long)groups * S * KW * 2 * ks <= cap && 2 * ks * S <= KC && (S > 1 || 8 * ks <= KC)) ks *= 2;
   }
   while (ks > 1 && ks * S > KC) ks /= 2;
   p.D = (o.ring >= 2 && o.ring <= 4) ? o.ring : ((p.MT == 1 && ks <= 2) ? 3 : 2);
