@@ -239,14 +239,13 @@ int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t
  * are never read into a result (they may hold anything, NaN included); rows up to it must be finite, since a
  * multi-token step reads whole 32-key blocks up to the largest position of the rows it groups. max_keys: an upper bound on positions[m] + 1 over
  * the calls that will run (sizes the launch; a captured graph keeps it; keys past it are still attended, by the last
- * key partition). Hq / Hkv in {1, 2, 4, 6, 7, 8}. workspace (optional, 16-byte aligned, at least 4096 bytes, the
- * first 4096 zero before the first call: arrival counters that every call leaves zero; from version 0.2 on -- 0.1
- * needed no initial contents): when there are too few
- * (token, head group) blocks to fill the GPU and max_keys >= 512, the keys are split into partitions whose fp32
- * partial softmax sums (blocks x partitions x (2 + 128) x 4 bytes after the counters, at most workspace_bytes) the
- * last block of each (token, head group) to finish merges in partition order (steps with at least 32 query rows per
- * KV head: a second launch merges them); the same bits on every call for a given launch. NULL = no split. Calls that
- * overlap on one workspace race. */
+ * key partition). Hq / Hkv in {1, 2, 4, 6, 7, 8}. workspace (optional, 16-byte aligned, at least 4096 bytes, no
+ * initial contents needed; its first 4096 bytes are not used -- version 0.2 kept arrival counters there and needed
+ * them zero): when there are too few (token, head group) blocks to fill the GPU and max_keys >= 512, the keys are
+ * split into partitions whose fp32 partial softmax sums (blocks x partitions x (2 + 128) x 4 bytes after the first
+ * 4096, at most workspace_bytes; steps with at least 32 query rows per KV head: 16-row tiles x partitions x
+ * (2 + 128) x 4) a second launch merges in partition order; the same bits on every call for a given launch. NULL = no
+ * split. Calls that overlap on one workspace race. */
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
                      size_t workspace_bytes, void* stream);

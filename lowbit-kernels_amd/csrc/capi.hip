@@ -184,7 +184,7 @@ using namespace lowbit;
 
 extern "C" {
 
-const char* lowbit_version(void) { return "lowbit_w4 0.2 gfx950"; }
+const char* lowbit_version(void) { return "lowbit_w4 0.3 gfx950"; }
 
 int lowbit_set_launch_override(int waves_per_group, int ring, int k_splits) {
   if (!(waves_per_group == 0 || waves_per_group == 1 || waves_per_group == 2 || waves_per_group == 4 ||

@@ -116,10 +116,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
 // probabilities never leave the lane that multiplies them into V. Waves take blocks of KB keys; the row groups and
 // the waves are merged at the end (lane shuffles, then LDS).
 // When (token, group) blocks alone cannot fill the chip (a decode step), the keys are also split into P partitions
-// of CH keys (grid.y): each block writes its partial (max, sum, unnormalized output) to the workspace with
-// agent-coherent stores (store_partial) and counts its arrival; the last of the P blocks of a (token, group) merges
-// the P partials in partition order (merge_partitions) and writes the output. (With a release per block, an L2
-// write-back, this merge measured slower than a second launch; the coherent stores need none.)
+// of CH keys (grid.y): each block writes its partial (max, sum, unnormalized output) to the workspace and
+// attention_combine, launched next, merges the P partials in partition order (merge_partitions). A merge by the last
+// block to arrive (agent-coherent partial stores, an arrival counter per (token, group)) measured slower in graph
+// decode (3B: 1.139 against 1.124 ms/token): phase stamps put 1.8 us on the arrival count alone, the P blocks of a
+// (token, group) incrementing one counter, and 2.6 us on the last block's merge, against ~3 us for the key loop.
 // Output dim d of one (block, head) from the P <= kAttnMaxParts partials [max, sum, o[128]] at float index `first`,
 // `stride` floats apart: max over partitions, then the rescaled sums in partition order (partitions that saw no key
 // hold max = -inf and are skipped; partition 0 always holds key 0). The loops run to the compile-time bound, so all
@@ -152,11 +153,10 @@ template <int G, int KB>
 __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k_cache, const f16* __restrict__ v_cache,
     const int64_t* __restrict__ pos, f16* __restrict__ out, int Hq, int Hkv, int L, float scale, int CH,
-    uint32_t* __restrict__ ctr, float* __restrict__ part) {
+    float* __restrict__ part) {
   constexpr int NI = KB / 4;                                 // 16-byte loads per lane and step, per K and per V
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ int s_last;
-  args_in_sgprs(q, k_cache, v_cache, pos, out, Hq, Hkv, L, CH, ctr, part, (int)blockDim.x);
+  args_in_sgprs(q, k_cache, v_cache, pos, out, Hq, Hkv, L, CH, part, (int)blockDim.x);
   const int groups = Hq / G, P = gridDim.y, pid = blockIdx.y;
   const int m = blockIdx.x / groups, h0 = (blockIdx.x % groups) * G, hk = h0 / (Hq / Hkv);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
@@ -243,8 +243,7 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
   }
   __syncthreads();
   // partial of this block: [G][2 + D] floats (max, sum, then the unnormalized output), per (token, group, partition)
-  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)(gridDim.x * P * G * (2 + kHeadDim) * 4));
-  const int mine = (blockIdx.x * P + pid) * G * (2 + kHeadDim);
+  float* mine = part + (size_t)(blockIdx.x * P + pid) * G * (2 + kHeadDim);
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
     const int g = idx / kHeadDim, d = idx % kHeadDim;
     float gm = -INFINITY;
@@ -260,33 +259,17 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
     if (P == 1) {
       out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
     } else {
-      const int at = 4 * (mine + g * (2 + kHeadDim));
-      store_partial(pr, at + 4 * (2 + d), num);
+      mine[g * (2 + kHeadDim) + 2 + d] = num;
       if (d == 0) {
-        store_partial(pr, at, gm);
-        store_partial(pr, at + 4, den);
+        mine[g * (2 + kHeadDim)] = gm;
+        mine[g * (2 + kHeadDim) + 1] = den;
       }
     }
   }
-  if (P == 1) return;
-  // count this block's arrival once its partials are acknowledged; the last of the P merges them
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(P - 1);
-  __syncthreads();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if (!s_last) return;
-  if (threadIdx.x == 0) __hip_atomic_store(ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
-    const int g = idx / kHeadDim, d = idx % kHeadDim;
-    out[((size_t)m * Hq + h0 + g) * kHeadDim + d] =
-        (f16)merge_partitions(pr, blockIdx.x * P * G * (2 + kHeadDim) + g * (2 + kHeadDim), G * (2 + kHeadDim), P, d);
-  }
 }
 
-// out[m][h][d] from the P <= kAttnMaxParts partials of attention_mfma (merge_partitions), launched after it
+// out[m][h][d] from the P <= kAttnMaxParts partials of attention_kernel or attention_mfma (merge_partitions), launched
+// after it
 __global__ __launch_bounds__(256) void attention_combine(const float* __restrict__ part, f16* __restrict__ out,
                                                          int blocks, int G, int P, int Hq) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -543,10 +526,9 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   const int max_waves = (G == 1 && KB == 32) ? 16 : 8;
   const long blocks = (long)M * (Hq / G);
   // key partitions: when the (token, group) blocks cannot fill the chip, split the keys so that about
-  // kAttnTargetBlocks blocks run, each with at least kAttnMinKeys keys, within the workspace and its counters
+  // kAttnTargetBlocks blocks run, each with at least kAttnMinKeys keys, within the workspace
   int P = 1;
-  if (ws && ws_bytes > kAttnCounterBytes && blocks < kAttnTargetBlocks && blocks <= (long)(kAttnCounterBytes / 4) &&
-      max_keys >= kAttnMinSplitKeys) {
+  if (ws && ws_bytes > kAttnCounterBytes && blocks < kAttnTargetBlocks && max_keys >= kAttnMinSplitKeys) {
     P = (int)std::min<long>({(kAttnTargetBlocks + blocks - 1) / blocks, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
                              (long)kAttnMaxParts});
     const size_t per = (size_t)blocks * G * (2 + kHeadDim) * sizeof(float);
@@ -560,10 +542,13 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   // costs more than the keys they share out (measured: 3B prompt of 512 tokens 58 -> 48 us, 7B 99 -> 70 us)
   if (blocks * P >= kAttnManyBlocks && waves > 4) waves = 4;
   const size_t lds = (size_t)waves * G * 2 * 4 + (size_t)waves * G * kHeadDim * 4;
-  uint32_t* ctr = static_cast<uint32_t*>(ws);
   float* part = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kAttnCounterBytes) : nullptr;
-  return launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos, out, Hq,
-                Hkv, L, scale, CH, ctr, part);
+  hipError_t e = launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos,
+                        out, Hq, Hkv, L, scale, CH, part);
+  if (e != hipSuccess || P == 1) return e;
+  const long threads = (long)M * Hq * kHeadDim;
+  return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, (int)blocks, G,
+                P, Hq);
 }
 // multi-token steps and prompts on MFMA: one wave per (KV head, 16 query rows, key partition); partitions while the
 // waves number fewer than kAttnMfmaTargetWaves, at most one per kAttnMinKeys of max_keys, within the workspace (each
@@ -580,7 +565,7 @@ hipError_t launch_attention_mfma(const f16* q, const f16* k, const f16* v, const
     const size_t per = (size_t)M * Hkv * G * (2 + kHeadDim) * sizeof(float);
     P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, (ws_bytes - kAttnCounterBytes) / per));
   }
-  // the partials after the decode kernel's arrival counters, which this kernel leaves untouched
+  // the partials after the workspace's first kAttnCounterBytes (unused, kept for the layout)
   float* part = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kAttnCounterBytes) : nullptr;
   hipError_t e = launch(attention_mfma, dim3((unsigned)waves, P), dim3(64), 0, st, q, k, v, pos, out, M, Hq, Hkv, L,
                         scale, part);

@@ -172,8 +172,8 @@ constexpr int kAttnTargetBlocks = 256;
 constexpr int kAttnMinKeys = 64;
 constexpr int kAttnMinSplitKeys = 512;
 constexpr int kAttnMaxParts = 16;
-// the attention workspace starts with this many bytes of arrival counters (one per (token, head group) block or MFMA
-// row tile that splits its keys; zero before the first call, left zero by every call), then the fp32 partials
+// the attention workspace's fp32 partials start this many bytes in (the bytes before them are not used; they held
+// arrival counters in an earlier version of the library, so callers size workspaces with them)
 constexpr size_t kAttnCounterBytes = 4096;
 // the MFMA attention takes steps with at least kAttnMfmaMinRows query rows (tokens x query heads per KV head), and
 // splits keys while its waves number fewer than kAttnMfmaTargetWaves

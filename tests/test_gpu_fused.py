@@ -252,10 +252,9 @@ def test_qkv_rope_rows_equal_projection_then_rope(cuda, hq, hkv, k, m):
                                                 (16, 2, 768, list(range(512, 528))), (16, 2, 600, list(range(100, 400))),
                                                 (12, 2, 300, list(range(0, 300, 37)))])
 def test_attention_against_fp32_softmax(cuda, hq, hkv, L, positions):
-    """Decode steps (a few tokens: one block per (token, head group), key partitions merged by the last block of
-    each (token, head group) to finish, through arrival counters at the workspace's head) and multi-token steps and
-    prompts (from 32 query rows per KV head: the MFMA kernel, with and without partitions, merged by a second
-    launch). Repeated calls give the same bits and leave the counters at zero."""
+    """Decode steps (a few tokens: one block per (token, head group), key partitions merged by a second launch) and
+    multi-token steps and prompts (from 32 query rows per KV head: the MFMA kernel, with and without partitions, merged
+    the same way). Repeated calls give the same bits, and the workspace's first 4096 bytes are left untouched."""
     g = torch.Generator(device="cuda").manual_seed(hq + L)
     m = len(positions)
     q = torch.randn(m, hq, 128, generator=g, device="cuda").half()
