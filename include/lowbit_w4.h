@@ -250,6 +250,26 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* One decoded token's attention and its output projection in two launches: y [1, N] = epilogue(attn [1, Hq * 128] .
+ * W^T) with attn what lowbit_attention computes for M = 1 (the same q, caches, positions, max_keys and scale), W the
+ * int4 MFMA-layout weight [N, Hq * 128] with its scales (group: a multiple of 128) or, for the _f16_ variant, an fp16
+ * weight [N, Hq * 128] row-major; epilogue and aux as in lowbit_w4_linear_fused (aux may be y for the residual). The
+ * attention keeps at most 8 key partitions and leaves their partial softmax sums in the workspace; the projection's
+ * prologue merges them into its x in partition order, the attention's own merge, so y has the bits of lowbit_attention
+ * (with a workspace that holds at most the same partitions) followed by lowbit_w4_linear_fused / lowbit_f16_linear_fused
+ * at M = 1 -- one launch fewer, and the attention output never written. Hq <= 32, Hq / Hkv in {1, 2, 4, 6, 7, 8};
+ * workspace required: 16-byte aligned, at least 4096 + Hq * 132 * 4 bytes, no initial contents (the partials, P x Hq
+ * x 132 x 4 bytes, follow its first 4096). No counterpart in the reference (its decoder runs torch attention, then
+ * W4Linear); it serves the fused decoder's one-token step. */
+int lowbit_w4_attention_linear(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions,
+                               int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, const void* w,
+                               const void* s, void* y, int64_t N, int64_t group, int epilogue, const void* aux,
+                               void* workspace, size_t workspace_bytes, void* stream);
+int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions,
+                                int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, const void* w,
+                                void* y, int64_t N, int epilogue, const void* aux, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* fp16 GEMV for the tied fp16 lm_head of a decode step (or the last row of a prefill): y [M, N] = fp16(x [M, K] . W^T)
  * with W fp16 [N, K] row-major, fp32 accumulation, 1 <= M <= 4, K % 8 == 0, M * K * 2 <= 65536, x and W 16-byte
  * aligned. No counterpart in the reference (its head is torch.nn.functional.linear, cuBLAS); it replaces that call

@@ -491,6 +491,55 @@ int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t
   return hip_status(gemm_prefill_launch(a, workspace, workspace ? workspace_bytes : 0), "w4_qkv_rope_rows");
 }
 
+// One token's attention followed by its output projection, the merge of the attention's key partitions done in the
+// projection's prologue (shared by the int4 and fp16-weight entry points below; w4: scales given, else fp16 weights)
+static int attention_linear_impl(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, int64_t Hq,
+                          int64_t Hkv, int64_t L, int64_t max_keys, float scale, const void* w, const void* s, void* y,
+                          int64_t N, int64_t group, int epilogue, const void* aux, void* workspace,
+                          size_t workspace_bytes, void* stream, const char* what) {
+  if (!q || !k_cache || !v_cache || !positions || !w || !y || !workspace) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || !fits_int(L * 128 * Hkv))
+    return fail(LOWBIT_ERR_SHAPE, "%s: Hq, Hkv (dividing Hq), L must be positive", what);
+  const int64_t g = Hq / Hkv, K = Hq * 128;
+  if (!(g == 1 || g == 2 || g == 4 || g == 6 || g == 7 || g == 8))
+    return fail(LOWBIT_ERR_SHAPE, "%s takes 1, 2, 4, 6, 7 or 8 query heads per KV head", what);
+  if (Hq > 32) return fail(LOWBIT_ERR_SHAPE, "%s takes at most 32 query heads (x of at most 4096)", what);
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(w))
+    return fail(LOWBIT_ERR_ALIGN, "%s needs 16-byte aligned q, caches and weights", what);
+  const size_t need = kAttnCounterBytes + (size_t)Hq * kAttnRec * 4;
+  if (!aligned16(workspace) || workspace_bytes < need)
+    return fail(LOWBIT_ERR_ARG, "%s: the workspace must be 16-byte aligned and hold at least %zu bytes", what, need);
+  if (N < 1 || !fits_int(N)) return fail(LOWBIT_ERR_SHAPE, "%s: N must be positive", what);
+  if (s) {
+    if (group % 128 || group < 128 || K % group) return fail(LOWBIT_ERR_LAYOUT, "%s: the group must be a multiple of 128 dividing K", what);
+    if (int rc = check_mfma_layout_limits(N, K, group, 1)) return rc;
+  }
+  if (epilogue < LOWBIT_EPI_STORE || epilogue > LOWBIT_EPI_SILU_MUL) return fail(LOWBIT_ERR_ARG, "unknown epilogue");
+  if ((epilogue == LOWBIT_EPI_BIAS || epilogue == LOWBIT_EPI_RESIDUAL) && !aux)
+    return fail(LOWBIT_ERR_ARG, "the bias and residual epilogues need aux");
+  if (epilogue == LOWBIT_EPI_SILU_MUL && (N % 16 || (reinterpret_cast<uintptr_t>(y) & 7)))
+    return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
+  if (int rc = check_device()) return rc;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  f16* xbuf = reinterpret_cast<f16*>(ws + kAttnCounterBytes);   // the attention's output when it runs unsplit
+  int parts = 1;
+  hipError_t e = attention_partials_launch(static_cast<const f16*>(q), static_cast<const f16*>(k_cache),
+                                           static_cast<const f16*>(v_cache), positions, xbuf, (int)Hq, (int)Hkv, (int)L,
+                                           (int)std::max<int64_t>(1, std::min(max_keys, L)), scale, workspace,
+                                           workspace_bytes, &parts, st);
+  if (e != hipSuccess) return hip_status(e, what);
+  GemvArgs a{xbuf, static_cast<const uint8_t*>(w), s ? static_cast<const f16*>(s) : xbuf, static_cast<f16*>(y), 1,
+             (int)N, (int)K, s ? (int)group : (int)K, st};
+  a.epi.mode = epilogue;
+  a.epi.aux = static_cast<const f16*>(aux);
+  if (parts > 1) {
+    a.epi.attn_part = reinterpret_cast<const float*>(ws + kAttnCounterBytes);
+    a.epi.attn_parts = parts;
+  }
+  return hip_status(s ? gemv_mfma_layout_launch(a, 0) : gemv_f16w_launch(a), what);
+}
+
 int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions, void* out,
                      int64_t M, int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, void* workspace,
                      size_t workspace_bytes, void* stream) {
@@ -510,6 +559,23 @@ int lowbit_attention(const void* q, const void* k_cache, const void* v_cache, co
                                      (int)Hq, (int)Hkv, (int)L, (int)std::max<int64_t>(1, std::min(max_keys, L)), scale,
                                      workspace, workspace ? workspace_bytes : 0, static_cast<hipStream_t>(stream)),
                     "attention");
+}
+
+int lowbit_w4_attention_linear(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions,
+                               int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, const void* w,
+                               const void* s, void* y, int64_t N, int64_t group, int epilogue, const void* aux,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (!s) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  return attention_linear_impl(q, k_cache, v_cache, positions, Hq, Hkv, L, max_keys, scale, w, s, y, N, group, epilogue,
+                               aux, workspace, workspace_bytes, stream, "w4_attention_linear");
+}
+
+int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* v_cache, const int64_t* positions,
+                                int64_t Hq, int64_t Hkv, int64_t L, int64_t max_keys, float scale, const void* w,
+                                void* y, int64_t N, int epilogue, const void* aux, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return attention_linear_impl(q, k_cache, v_cache, positions, Hq, Hkv, L, max_keys, scale, w, nullptr, y, N, 0,
+                               epilogue, aux, workspace, workspace_bytes, stream, "f16_attention_linear");
 }
 
 int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {

@@ -11,7 +11,7 @@ namespace lowbit {
 
 namespace {
 
-constexpr int kHeadDim = 128;
+constexpr int kHeadDim = kAttnHeadDim;
 
 __device__ __forceinline__ float block_sum(float v, float* red) {    // all threads of the block get the total
   v = wave_sum(v);
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const f16* __restrict__ qk
 // block to arrive (agent-coherent partial stores, an arrival counter per (token, group)) measured slower in graph
 // decode (3B: 1.139 against 1.124 ms/token): phase stamps put 1.8 us on the arrival count alone, the P blocks of a
 // (token, group) incrementing one counter, and 2.6 us on the last block's merge, against ~3 us for the key loop.
-// Output dim d of one (block, head) from the P <= kAttnMaxParts partials [max, sum, o[128]] at float index `first`,
+// Output dim d of one (block, head) from the P <= kAttnMaxParts partial records (kAttnRec floats) at float index `first`,
 // `stride` floats apart: max over partitions, then the rescaled sums in partition order (partitions that saw no key
 // hold max = -inf and are skipped; partition 0 always holds key 0). The loops run to the compile-time bound, so all
 // the loads are requested before the first is used.
@@ -133,7 +133,7 @@ __device__ __forceinline__ float merge_partitions(__amdgpu_buffer_rsrc_t pr, int
     const bool live = p < P;
     pm[p] = live ? load_partial(pr, at) : -INFINITY;
     ps[p] = live ? load_partial(pr, at + 4) : 0.f;
-    po[p] = live ? load_partial(pr, at + 4 * (2 + d)) : 0.f;
+    po[p] = live ? load_partial(pr, at + 4 * (4 + d)) : 0.f;
   }
   float gm = -INFINITY;
 #pragma unroll
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
   }
   __syncthreads();
   // partial of this block: [G][2 + D] floats (max, sum, then the unnormalized output), per (token, group, partition)
-  float* mine = part + (size_t)(blockIdx.x * P + pid) * G * (2 + kHeadDim);
+  float* mine = part + (size_t)(blockIdx.x * P + pid) * G * kAttnRec;
   for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
     const int g = idx / kHeadDim, d = idx % kHeadDim;
     float gm = -INFINITY;
@@ -259,10 +259,10 @@ __global__ __launch_bounds__(G == 1 && KB == 32 ? 1024 : 512) void attention_ker
     if (P == 1) {
       out[((size_t)m * Hq + h0 + g) * kHeadDim + d] = (f16)(num / den);
     } else {
-      mine[g * (2 + kHeadDim) + 2 + d] = num;
+      mine[g * kAttnRec + 4 + d] = num;
       if (d == 0) {
-        mine[g * (2 + kHeadDim)] = gm;
-        mine[g * (2 + kHeadDim) + 1] = den;
+        mine[g * kAttnRec] = gm;
+        mine[g * kAttnRec + 1] = den;
       }
     }
   }
@@ -276,9 +276,9 @@ __global__ __launch_bounds__(256) void attention_combine(const float* __restrict
   if (idx >= blocks * G * kHeadDim) return;
   const int b = idx / (G * kHeadDim), g = (idx / kHeadDim) % G, d = idx % kHeadDim;
   const int groups = Hq / G, m = b / groups, h = (b % groups) * G + g;
-  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)(blocks * P * G * (2 + kHeadDim) * 4));
+  const __amdgpu_buffer_rsrc_t pr = make_rsrc(part, (uint32_t)(blocks * P * G * kAttnRec * 4));
   out[((size_t)m * Hq + h) * kHeadDim + d] =
-      (f16)merge_partitions(pr, b * P * G * (2 + kHeadDim) + g * (2 + kHeadDim), G * (2 + kHeadDim), P, d);
+      (f16)merge_partitions(pr, b * P * G * kAttnRec + g * kAttnRec, G * kAttnRec, P, d);
 }
 
 // Causal GQA attention on MFMA for multi-token steps and prompts (same contract as attention_kernel): one wave per
@@ -415,15 +415,13 @@ __global__ __launch_bounds__(64) void attention_mfma(const f16* __restrict__ q, 
     }
     return;
   }
-  float* mine = part + (((size_t)(m * Hkv + hk) * P + pid) * G + g) * (2 + kHeadDim);
+  float* mine = part + (((size_t)(m * Hkv + hk) * P + pid) * G + g) * kAttnRec;
   if (c == 0) {
     mine[0] = mx;
     mine[1] = lsum;
   }
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) mine[2 + 16 * dt + 4 * c + v] = o[dt][v];
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(mine + 4 + 16 * dt + 4 * c) = o[dt];
 }
 
 // fp16 GEMV for the (tied) lm_head, M <= 4: y[m][n] = fp16(sum_k x[m][k] W[n][k]), W fp16 [N][K] row-major, fp32
@@ -520,9 +518,12 @@ hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_f
 }
 
 namespace {
+// combine = false: the partials are left for the caller (their count in *parts; with one partition the kernel writes
+// out itself and *parts is 1)
 template <int G, int KB>
 hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
-                            int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st) {
+                            int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st,
+                            int max_parts = kAttnMaxParts, bool combine = true, int* parts = nullptr) {
   const int max_waves = (G == 1 && KB == 32) ? 16 : 8;
   const long blocks = (long)M * (Hq / G);
   // key partitions: when the (token, group) blocks cannot fill the chip, split the keys so that about
@@ -530,8 +531,8 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   int P = 1;
   if (ws && ws_bytes > kAttnCounterBytes && blocks < kAttnTargetBlocks && max_keys >= kAttnMinSplitKeys) {
     P = (int)std::min<long>({(kAttnTargetBlocks + blocks - 1) / blocks, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
-                             (long)kAttnMaxParts});
-    const size_t per = (size_t)blocks * G * (2 + kHeadDim) * sizeof(float);
+                             (long)max_parts});
+    const size_t per = (size_t)blocks * G * kAttnRec * sizeof(float);
     P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, (ws_bytes - kAttnCounterBytes) / per));
   }
   const int CH = ((max_keys + P - 1) / P + KB - 1) / KB * KB;   // keys per partition, whole steps
@@ -543,9 +544,10 @@ hipError_t launch_attention(const f16* q, const f16* k, const f16* v, const int6
   if (blocks * P >= kAttnManyBlocks && waves > 4) waves = 4;
   const size_t lds = (size_t)waves * G * 2 * 4 + (size_t)waves * G * kHeadDim * 4;
   float* part = ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kAttnCounterBytes) : nullptr;
+  if (parts) *parts = P;
   hipError_t e = launch(attention_kernel<G, KB>, dim3((unsigned)blocks, P), dim3(64 * waves), lds, st, q, k, v, pos,
                         out, Hq, Hkv, L, scale, CH, part);
-  if (e != hipSuccess || P == 1) return e;
+  if (e != hipSuccess || P == 1 || !combine) return e;
   const long threads = (long)M * Hq * kHeadDim;
   return launch(attention_combine, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, part, out, (int)blocks, G,
                 P, Hq);
@@ -562,7 +564,7 @@ hipError_t launch_attention_mfma(const f16* q, const f16* k, const f16* v, const
   if (ws && ws_bytes > kAttnCounterBytes && waves < kAttnMfmaTargetWaves && max_keys >= 2 * kAttnMinKeys) {
     P = (int)std::min<long>({(kAttnMfmaTargetWaves + waves - 1) / waves, (max_keys + kAttnMinKeys - 1) / kAttnMinKeys,
                              (long)kAttnMaxParts});
-    const size_t per = (size_t)M * Hkv * G * (2 + kHeadDim) * sizeof(float);
+    const size_t per = (size_t)M * Hkv * G * kAttnRec * sizeof(float);
     P = (int)std::max<size_t>(1, std::min<size_t>((size_t)P, (ws_bytes - kAttnCounterBytes) / per));
   }
   // the partials after the workspace's first kAttnCounterBytes (unused, kept for the layout)
@@ -591,6 +593,15 @@ hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int6
     case 8: return launch_attention<8, 32>(q, k, v, pos, out, M, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t attention_partials_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int Hq,
+                                     int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, int* parts,
+                                     hipStream_t st) {
+  // one token: the decode kernel with one query head per block (the MFMA kernel takes 32 or more rows per KV head)
+  if (Hq / Hkv >= kAttnMfmaMinRows || Hkv >= 64) return hipErrorInvalidValue;
+  return launch_attention<1, 32>(q, k, v, pos, out, 1, Hq, Hkv, L, max_keys, scale, ws, ws_bytes, st, kAttnXMaxParts,
+                                 false, parts);
 }
 
 }  // namespace lowbit

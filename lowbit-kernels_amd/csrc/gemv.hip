@@ -60,11 +60,17 @@ __device__ __forceinline__ float dot32(const u32x4& wv, const u32x4 (&xv)[4]) {
 // registers are decoded. x, the scales and the norm weights also arrive by direct-to-LDS loads, so the compiler issues
 // no vector-memory load before the main loop and every wait on the ring is counted by hand (see dma16).
 //
+// kAttnX (M = 1, register ring, x in LDS, fused): x is an attention step's output, merged here from the records of its
+// key partitions (attention_partials_launch) instead of read: thread t < K / 4 loads the records of head t / 32,
+// merges dims 4 t .. 4 t + 3 with the arithmetic of the attention's own merge (merge_partitions: the same bits) and
+// writes them to LDS; one barrier later the zero-weight sums are taken from LDS. This replaces the attention's merge
+// launch and its output round trip (one launch fewer per decoded token and layer).
 // kF16 (M = 1, R = 1, register ring, x in LDS): the same kernel over an fp16 weight [N, K] in row-major order, the
 // comparator the W4A16 decode is measured against (same tiles, waves, tile splits, prologue, reduction and epilogues;
 // only the weight bytes differ). A wave-load is then 16 rows x 32 k (64 contiguous bytes per row): lane (r, q) takes
 // k = 32 p + 8 q .. + 7 of row r for sub-load p, 4 dot2 against x; no scales, no zero sums.
-template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1, int LR = 0, bool kF16 = false>
+template <int M, int R, int D, bool kLdsX, bool kFused = false, int CS = 1, int LR = 0, bool kF16 = false,
+          bool kAttnX = false>
 __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(const f16* __restrict__ x,
                                                                            const uint8_t* __restrict__ w,
                                                                            const f16* __restrict__ s,
@@ -74,12 +80,13 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   static_assert(CS == 1 || (R == 1 && (CS == 2 || CS == 4)), "a tile splits over 2 or 4 workgroups, one tile each");
   static_assert(LR == 0 || (M == 1 && R == 1 && kLdsX), "the LDS ring serves the one-row, one-tile GEMV");
   static_assert(!kF16 || (M == 1 && R == 1 && LR == 0 && kLdsX), "the fp16-weight mode serves the one-row GEMV");
+  static_assert(!kAttnX || (M == 1 && R == 1 && LR == 0 && kLdsX && kFused), "x from attention partials: one row");
   constexpr int RS = 16 / CS;                               // rows of a tile one workgroup owns
   constexpr int XB = M == 1 ? 2 : 1;                        // x blocks (32 k) staged per thread before the ring
   constexpr int kScaleLoads = 4;                            // scales per thread requested before the ring
   // norm_w (M = 1 with x in LDS only; the launcher then gives every block of x a thread): the projection's input is
   // RMSNorm(x) * norm_w, computed here exactly as lowbit_rmsnorm does (fp32 statistics, fp16 roundings)
-  const bool norm = kFused && kLdsX && M == 1 && norm_w != nullptr;   // kFused: epilogue / norm code compiled in
+  const bool norm = !kAttnX && kFused && kLdsX && M == 1 && norm_w != nullptr;   // kFused: epilogue / norm compiled in
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   args_in_sgprs(x, w, s, N, K, G, (int)blockDim.x);
   if constexpr (kFused) args_in_sgprs(epi.aux, norm_w);    // the epilogue's and the norm's argument lines too
@@ -108,8 +115,30 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
   const int nb = M * (K / 32), ns = kF16 ? 0 : nrows * KG;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s + (size_t)n0 * KG, (uint32_t)(ns * 2));
+  // kAttnX: x piece t (dims 4 t .. 4 t + 3, head t / 32) from its head's records (max, sum, -, -, output[128]); the
+  // loads of this thread's first piece go out before everything else, further pieces (K / 4 > threads) in staging.
+  // Partitions past attn_parts and pieces past K / 4 read nothing (max -inf: skipped by the merge).
+  float apm[kAttnX ? kAttnXMaxParts : 1], aps[kAttnX ? kAttnXMaxParts : 1];
+  f32x4 apo[kAttnX ? kAttnXMaxParts : 1];
+  const __amdgpu_buffer_rsrc_t ar =
+      make_rsrc(epi.attn_part, kAttnX ? (uint32_t)((K >> 7) * epi.attn_parts * kAttnRec * 4) : 0u);
+  auto attn_load = [&](int t) {
+    const int P = epi.attn_parts, rec0 = (t >> 5) * P * kAttnRec * 4;
+    const bool tl = t < (K >> 2);
+#pragma unroll
+    for (int p = 0; p < kAttnXMaxParts; ++p) {
+      const bool live = tl && p < P;
+      const int rec = rec0 + p * kAttnRec * 4;
+      const float mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ar, live ? rec : kOutOfRange, 0, 0));
+      aps[p] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ar, live ? rec + 4 : kOutOfRange, 0, 0));
+      apo[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, live ? rec + 16 + 16 * (t & 31) : kOutOfRange,
+                                                                            0, 0));
+      apm[p] = live ? mv : -INFINITY;
+    }
+  };
+  if constexpr (kAttnX) attn_load((int)threadIdx.x);
   u32x4 xst[XB][4], wst[XB][4];
-  if (LR == 0 && kLdsX) {
+  if (LR == 0 && kLdsX && !kAttnX) {
 #pragma unroll
     for (int u = 0; u < XB; ++u) {
       const int b = (int)threadIdx.x + u * (int)blockDim.x;
@@ -260,7 +289,34 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       }
     }
   }
-  if (LR > 0) {                                            // x is in LDS (normalized in registers when norm)
+  if (kAttnX) {                                            // merge x into LDS, then its zero-weight sums from there
+    for (int t = (int)threadIdx.x; t < (K >> 2); t += blockDim.x) {
+      if (t != (int)threadIdx.x) attn_load(t);
+      float gm = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < kAttnXMaxParts; ++p) gm = fmaxf(gm, apm[p]);
+      float num[4] = {0.f, 0.f, 0.f, 0.f}, den = 0.f;
+#pragma unroll
+      for (int p = 0; p < kAttnXMaxParts; ++p) {
+        if (apm[p] == -INFINITY) continue;                  // a partition that saw no key
+        const float f = expf(apm[p] - gm);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] = fmaf(f, apo[p][e], num[e]);
+        den = fmaf(f, aps[p], den);
+      }
+      const f16x2 lo = {(f16)(num[0] / den), (f16)(num[1] / den)}, hi = {(f16)(num[2] / den), (f16)(num[3] / den)};
+      *reinterpret_cast<uint2*>(lds_x + 4 * t) = make_uint2(as_u32(lo), as_u32(hi));
+    }
+    __syncthreads();
+    if constexpr (!kF16) {
+      for (int b = (int)threadIdx.x; b < nb; b += blockDim.x) {
+        u32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = reinterpret_cast<const u32x4*>(lds_x)[4 * b + j];
+        stage_block(b, v, false);
+      }
+    }
+  } else if (LR > 0) {                                     // x is in LDS (normalized in registers when norm)
     if (norm) {
 #pragma unroll
       for (int u = 0; u < XB; ++u) {
@@ -583,6 +639,9 @@ hipError_t launch_f16w(const GemvArgs& a, int waves) {
   const int ntiles = (a.N + 15) / 16;
   dim3 grid(CS == 1 ? ntiles : ntiles * CS), block(64 * waves);
   const size_t bytes = std::max<size_t>((size_t)a.K * 2, (size_t)waves * 16 * 4);
+  if (a.epi.attn_part)
+    return launch(gemv_mfma_layout<1, 1, 4, true, true, CS, 0, true, true>, grid, block, bytes, a.stream, a.x, a.w, a.s,
+                  a.y, a.N, a.K, a.K, a.epi, a.norm_w, a.eps);
   return launch(gemv_mfma_layout<1, 1, 4, true, true, CS, 0, true>, grid, block, bytes, a.stream, a.x, a.w, a.s, a.y,
                 a.N, a.K, a.K, a.epi, a.norm_w, a.eps);
 }
@@ -596,6 +655,14 @@ hipError_t launch_mfma_layout(const GemvArgs& a, int waves) {
   const size_t red_bytes = (size_t)waves * R * M * 16 * 4;
   const bool fused = a.epi.mode != kEpiStore || a.norm_w;
   if constexpr (M == 1) {                                    // only the M = 1 path carries epilogues and the norm
+    if constexpr (R == 1 && D == 4) {
+      if (a.epi.attn_part) {                                  // x merged from attention partials (kAttnX)
+        if (x_bytes + s_bytes > kGemvLdsX) return hipErrorInvalidValue;
+        return launch(gemv_mfma_layout<1, 1, 4, true, true, CS, 0, false, true>, grid, block,
+                      std::max(x_bytes + s_bytes, red_bytes), a.stream, a.x, a.w, a.s, a.y, a.N, a.K, a.G, a.epi,
+                      a.norm_w, a.eps);
+      }
+    }
     if (fused) {
       if (x_bytes + s_bytes <= kGemvLdsX)
         return launch(gemv_mfma_layout<M, R, D, true, true, CS>, grid, block, std::max(x_bytes + s_bytes, red_bytes),
@@ -714,6 +781,10 @@ hipError_t gemv_mfma_layout_launch(const GemvArgs& a, int rows_per_wave) {
   if (a.norm_w) {                                             // every 32-k block of x held by a thread (2 per thread)
     const int need = (a.K / 32 + 127) / 128;
     while (p.waves < need) p.waves *= 2;
+  }
+  if (a.epi.attn_part) {                                      // the plan of x as given, on the register ring
+    if (a.M != 1 || p.R != 1) return hipErrorInvalidValue;
+    return dispatch_mfma_layout<1>(a, 1, p.waves, 4, p.CS);
   }
   if (p.LR > 0 && a.M == 1 && (int64_t)a.N * (a.K / a.G) % 8 == 0 &&
       gemv_ring_lds(a.K, a.K / a.G, 16 / p.CS, p.waves, p.LR, a.norm_w).total <= kLdsPerCu) {

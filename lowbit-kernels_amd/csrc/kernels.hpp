@@ -30,6 +30,10 @@ struct Epilogue {
   int mode = kEpiStore;
   const f16* aux = nullptr;
   RopeArgs rope;
+  // one-row GEMV whose x is the merge of an attention step's key partitions (attention_partials_launch): the records
+  // [head][partition] of kAttnRec floats, attn_parts partitions per head (2 .. kAttnXMaxParts); nullptr: x as given
+  const float* attn_part = nullptr;
+  int attn_parts = 0;
 };
 
 // Four outputs of the kEpiRopeQKV epilogue, packed fp16, and where they go (dst == nullptr: nothing to store): dims
@@ -172,6 +176,12 @@ constexpr int kAttnTargetBlocks = 256;
 constexpr int kAttnMinKeys = 64;
 constexpr int kAttnMinSplitKeys = 512;
 constexpr int kAttnMaxParts = 16;
+// key partitions hand their partial softmax sums over in records of kAttnRec floats: the max, the sum, two unused
+// (the output then starts 16-byte aligned) and the unnormalized output of the head's kAttnHeadDim dims
+constexpr int kAttnHeadDim = 128;
+constexpr int kAttnRec = 4 + kAttnHeadDim;
+// the one-row GEMV that merges an attention step's partials into its x holds at most this many partitions per head
+constexpr int kAttnXMaxParts = 8;
 // the attention workspace's fp32 partials start this many bytes in (the bytes before them are not used; they held
 // arrival counters in an earlier version of the library, so callers size workspaces with them)
 constexpr size_t kAttnCounterBytes = 4096;
@@ -229,6 +239,12 @@ hipError_t hbm_read_launch(const void* src, size_t bytes, uint32_t* sink, int bl
 hipError_t hbm_copy_launch(const void* src, void* dst, size_t bytes, int blocks, hipStream_t stream);
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,
                             int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, hipStream_t st);
+// one token's attention without the merge of its key partitions: their records (kAttnRec floats, [head][partition])
+// start kAttnCounterBytes into ws and their count goes to *parts (<= kAttnXMaxParts); with one partition out is
+// written instead and *parts is 1
+hipError_t attention_partials_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int Hq,
+                                     int Hkv, int L, int max_keys, float scale, void* ws, size_t ws_bytes, int* parts,
+                                     hipStream_t st);
 hipError_t dequant_launch(const uint8_t* w, const f16* s, f16* out, int N, int K, int G, bool mfma, hipStream_t st);
 hipError_t relayout_launch(const uint8_t* src, uint8_t* dst, int N, int K, bool mfma, hipStream_t st);
 hipError_t quantize_launch(const void* w, int dtype, uint8_t* packed, f16* scales, int N, int K, int G,

@@ -52,6 +52,10 @@ SIGNATURES = {
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "lowbit_w4_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _i64,
+                                    _i64, _int, _vp, _vp, ctypes.c_size_t, _vp], _int),
+    "lowbit_f16_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _i64, _int,
+                                     _vp, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_f16_linear_fused": ([_vp, _vp, _vp, _i64, _i64, _int, _vp, _vp, ctypes.c_float, _vp], _int),
     "lowbit_f16_qkv_rope": ([_vp, _vp, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                              _i64, _vp], _int),
@@ -480,6 +484,53 @@ class NativeExt:
                                             hq, hkv, k_cache.shape[1], int(max_keys), float(scale),
                                             ptr(ws) if ws is not None else None, ws.numel() if ws is not None else 0,
                                             st))
+
+    def _attention_linear(self, q, k_cache, v_cache, positions, hq, hkv, max_keys, scale, w, s, group, epilogue, aux,
+                          out):
+        import torch
+        if not q.is_cuda or q.dim() != 3 or k_cache.dim() != 3:
+            raise RuntimeError("q [1, Hq, 128] and the caches [Hkv, L, 128] must be CUDA tensors")
+        _need(q, "q", torch.float16, (1, hq, 128), q.device)
+        _need(k_cache, "k_cache", torch.float16, (hkv, k_cache.shape[1], 128), q.device)
+        _need(v_cache, "v_cache", torch.float16, tuple(k_cache.shape), q.device)
+        _need(positions, "positions", torch.int64, (1,), q.device)
+        k = hq * 128
+        if s is not None:
+            _check_tensors(torch.empty((1, k), dtype=torch.float16, device=q.device), w, s, group)
+        elif w.dtype != torch.float16 or w.dim() != 2 or w.shape[1] != k or not w.is_contiguous() or w.device != q.device:
+            raise RuntimeError("w must be a contiguous float16 [N, Hq * 128] tensor on q's GPU")
+        n = w.shape[0]
+        cols = n // 2 if epilogue == EPI_SILU_MUL else n
+        y = out if out is not None else torch.empty((1, cols), dtype=torch.float16, device=q.device)
+        _need(y, "out", torch.float16, (1, cols), q.device)
+        _check_epilogue(epilogue, aux, 1, n, q.device)
+        with _DeviceGuard(q.device):
+            st = _stream(q.device)
+            ws = workspace(q.device, st, ATTENTION_WORKSPACE_BYTES)
+            common = (ptr(q), ptr(k_cache), ptr(v_cache), ptr(positions), hq, hkv, k_cache.shape[1], int(max_keys),
+                      float(scale))
+            aux_p = ptr(aux) if aux is not None else None
+            if s is not None:
+                check(self.lib.lowbit_w4_attention_linear(*common, ptr(w), ptr(s), ptr(y), n, group, int(epilogue), aux_p,
+                                                          ptr(ws), ws.numel(), st))
+            else:
+                check(self.lib.lowbit_f16_attention_linear(*common, ptr(w), ptr(y), n, int(epilogue), aux_p, ptr(ws),
+                                                           ws.numel(), st))
+        return y
+
+    def w4_attention_linear(self, q, k_cache, v_cache, positions, hq, hkv, max_keys, scale, w, s, group, epilogue,
+                            aux=None, out=None):
+        """One token's attention (as attention(), at most 8 key partitions) followed by the int4 projection with its
+        epilogue, the partitions merged in the projection's prologue (lowbit_w4_attention_linear): y [1, N] (or
+        [1, N / 2] for EPI_SILU_MUL); `out` may be `aux` for the residual."""
+        return self._attention_linear(q, k_cache, v_cache, positions, hq, hkv, max_keys, scale, w, s, group, epilogue,
+                                      aux, out)
+
+    def f16_attention_linear(self, q, k_cache, v_cache, positions, hq, hkv, max_keys, scale, w, epilogue, aux=None,
+                             out=None):
+        """w4_attention_linear over an fp16 weight W [N, Hq * 128] (lowbit_f16_attention_linear)."""
+        return self._attention_linear(q, k_cache, v_cache, positions, hq, hkv, max_keys, scale, w, None, 0, epilogue,
+                                      aux, out)
 
     def f16_gemv(self, x, w, out=None):
         """fp16 x [M <= 4, K] times fp16 W [N, K]^T -> fp16 [M, N] (fp32 accumulation)."""

@@ -209,9 +209,19 @@ class FusedQwen2:
                 qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
                 ext.rope_kv(qkv, positions, self.inv_freq, q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv,
                             permuted=self.quant in ("int4", "fp16_gemv"))
-            ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
-                          self.scale)
-            lay["o"](attn, EPI_RESIDUAL, h, out=h)
+            if fuse and self.hq <= 32:                        # the key partitions merged in the o projection
+                o = lay["o"]
+                if self.quant == "int4":
+                    ext.w4_attention_linear(q, self.k_cache[i], self.v_cache[i], positions, self.hq, self.hkv,
+                                            self.max_len, self.scale, o.wq.packed_mma, o.wq.scales, o.wq.group,
+                                            EPI_RESIDUAL, h, out=h)
+                else:
+                    ext.f16_attention_linear(q, self.k_cache[i], self.v_cache[i], positions, self.hq, self.hkv,
+                                             self.max_len, self.scale, o.w, EPI_RESIDUAL, h, out=h)
+            else:
+                ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
+                              self.scale)
+                lay["o"](attn, EPI_RESIDUAL, h, out=h)
             if fuse:
                 act = lay["gu"](h, EPI_SILU_MUL, norm=(lay["post_norm"], self.eps))
             else:
