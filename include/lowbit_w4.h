@@ -164,8 +164,9 @@ int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int lay
  * otherwise the MFMA GEMM; workspace as for lowbit_w4_gemm_mfma). Each mode rounds as the unfused torch ops do
  * (the projection to fp16 first; silu in fp32 then fp16, the product fp16), so results equal the unfused sequence
  * (nn.Linear bias add of the reference's W4Linear, lowbit/model.py:25-26; the residual add and silu(gate) * up of
- * transformers' Qwen2 layer). norm_weight (may be NULL; M = 1 and K <= 16384 only): project
- * lowbit_rmsnorm(x, norm_weight, eps) instead of x, the norm computed in the GEMV's prologue. */
+ * transformers' Qwen2 layer). norm_weight (may be NULL; 16-byte aligned; K <= 16384 at M = 1, K <= 8192 at M >= 2): project
+ * lowbit_rmsnorm(x, norm_weight, eps) instead of x, the norm computed in the kernel's prologue with lowbit_rmsnorm's
+ * arithmetic (the same bits as lowbit_rmsnorm followed by the projection). */
 int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
                            int64_t group, int epilogue, const void* aux, const void* norm_weight, float eps,
                            void* workspace, size_t workspace_bytes, void* stream);
@@ -224,7 +225,9 @@ int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* tab
 
 /* lowbit_w4_qkv_rope for M >= 1 tokens (a multi-token step or a prompt; no counterpart in the reference; it replaces
  * lowbit_w4_linear_fused / lowbit_w4_gemm_prefill with LOWBIT_EPI_BIAS followed by lowbit_rope_kv). x [M, K] is
- * the normalized layer input; token m's q -> q_out [M][Hq][128], its k and v -> the caches' row positions[m];
+ * the layer input, normalized here when norm_weight is given (RMSNorm(x) * norm_weight with lowbit_rmsnorm's
+ * arithmetic, each row's 1 / RMS over all of K; up to 64 rows, K <= 8192, the weight 16-byte aligned; NULL: x is
+ * already normalized); token m's q -> q_out [M][Hq][128], its k and v -> the caches' row positions[m];
  * rope_table is lowbit_rope_table's output for these positions. Up to 64 rows run the MFMA GEMM, more the prefill
  * GEMM; the workspace is that kernel's (as lowbit_w4_gemm_mfma or lowbit_w4_gemm_prefill; NULL = no K split). The
  * same bits as the unfused pair; more than 64 rows require (M + 128) * K * 2 < 2^31; the table 16-byte aligned,
@@ -232,6 +235,7 @@ int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* tab
 int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t M, int64_t N, int64_t K,
                             int64_t group, const void* bias, const int64_t* positions, const void* rope_table,
                             void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv, int64_t L,
+                            const void* norm_weight, float eps,
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Causal GQA attention: out[M][Hq * 128] for queries q [M][Hq][128] at positions[m] over cache rows 0..positions[m]

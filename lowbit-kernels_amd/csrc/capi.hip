@@ -322,8 +322,9 @@ int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y,
     return fail(LOWBIT_ERR_SHAPE, "silu-mul needs N (gate and up rows) a multiple of 16 and an 8-byte aligned y");
   if (workspace && (!aligned16(workspace) || workspace_bytes < kCounterBytes))
     return fail(LOWBIT_ERR_ARG, "the workspace must be 16-byte aligned and hold at least %zu bytes", kCounterBytes);
-  if (norm_weight && (M != 1 || K > 16384 || !aligned16(norm_weight)))
-    return fail(LOWBIT_ERR_ARG, "the fused input norm takes one row (M = 1), K <= 16384 and a 16-byte aligned weight");
+  if (norm_weight && (K > (M == 1 ? 16384 : 8192) || !aligned16(norm_weight)))
+    return fail(LOWBIT_ERR_ARG, "the fused input norm takes K <= 16384 (one row) or K <= 8192 (2..64 rows) and a 16-byte "
+                                "aligned weight");
   if (int rc = check_device()) return rc;
   GemvArgs a{static_cast<const f16*>(x), static_cast<const uint8_t*>(w), static_cast<const f16*>(s), static_cast<f16*>(y),
              (int)M, (int)N, (int)K, (int)group, static_cast<hipStream_t>(stream)};
@@ -464,9 +465,11 @@ int lowbit_rope_table(const int64_t* positions, const float* inv_freq, void* tab
 int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t M, int64_t N, int64_t K,
                             int64_t group, const void* bias, const int64_t* positions, const void* rope_table,
                             void* q_out, void* k_cache, void* v_cache, int64_t Hq, int64_t Hkv, int64_t L,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+                            const void* norm_weight, float eps, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = check_common(x, w, s, q_out, M, N, K, group)) return rc;
   if (M < 1) return fail(LOWBIT_ERR_ROWS, "qkv_rope_rows takes at least one row");
+  if (norm_weight && (M > 64 || K > 8192 || !aligned16(norm_weight)))
+    return fail(LOWBIT_ERR_ARG, "the fused input norm takes at most 64 rows, K <= 8192 and a 16-byte aligned weight");
   if (!bias || !positions || !rope_table || !k_cache || !v_cache) return fail(LOWBIT_ERR_ARG, "null pointer argument");
   if (Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || N != (Hq + 2 * Hkv) * 128 || !fits_int(L * 128 * Hkv) ||
       !fits_int(M * Hq * 128))
@@ -487,6 +490,8 @@ int lowbit_w4_qkv_rope_rows(const void* x, const void* w, const void* s, int64_t
   a.epi.aux = static_cast<const f16*>(bias);
   a.epi.rope = RopeArgs{positions, nullptr, static_cast<const uint32_t*>(rope_table), static_cast<f16*>(q_out),
                         static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), (int)Hq, (int)Hkv, (int)L};
+  a.norm_w = static_cast<const f16*>(norm_weight);
+  a.eps = eps;
   if (M <= 64) return hip_status(gemm_mfma_launch(a, 0, workspace, workspace ? workspace_bytes : 0), "w4_qkv_rope_rows");
   return hip_status(gemm_prefill_launch(a, workspace, workspace ? workspace_bytes : 0), "w4_qkv_rope_rows");
 }

@@ -60,14 +60,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16* __restrict__ x,
   for (int i = threadIdx.x * 8 + kNormPieces * step; i < H; i += step) add_squares(*reinterpret_cast<const u32x4*>(x + row + i));
   const float r = rsqrtf(block_sum(ss, red) / (float)H + eps);
   auto store_norm = [&](int i, const u32x4& v, const u32x4& g) {
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const f16x2 p = as_f16x2(v[j]), wj = as_f16x2(g[j]);
-      const f16x2 n = {(f16)((float)p[0] * r), (f16)((float)p[1] * r)};
-      o[j] = as_u32(f16x2{(f16)((float)wj[0] * (float)n[0]), (f16)((float)wj[1] * (float)n[1])});
-    }
-    *reinterpret_cast<u32x4*>(out + row + i) = o;
+    *reinterpret_cast<u32x4*>(out + row + i) = rms_apply8(v, g, r);
   };
 #pragma unroll
   for (int c = 0; c < kNormPieces; ++c) {

@@ -47,6 +47,8 @@ constexpr int kXPitch = 256;       // bytes per staged activation row (one 128-k
 // of these layouts. In the kernel: 7B gate/up at M = 64 22.8 -> 21.0 us, 7B down 32.3 -> 31.5, 3B merged gate|up
 // 15.4 -> 14.8 (a few shapes at 48 rows lose up to 3%: 2048 x 11008 9.5 -> 9.85).
 constexpr int xswz(int r) { return ((r & 3) << 2) | (r >> 2); }
+constexpr int kTilesNormMaxMT = 3;           // gemm_mfma_tiles normalizes its input up to 48 rows
+constexpr size_t kGemmMaxLds = 144 * 1024;   // dynamic LDS of a row-group workgroup: 128 KB of x buffers + 16 KB of norm weights
 }  // namespace
 
 template <int MT, int RW, int D, int KS, int TW, bool ROPE>
@@ -96,15 +98,22 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   }
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)N * (uint32_t)KG * 2u);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  // the input RMSNorm (epi.norm_w): each x piece is normalized as it is staged, with its row's 1 / RMS (s_rn, over all
+  // of K) and the norm weights of its 8 columns (the split's chunks of them staged in LDS after the x buffers, lds_g)
+  const bool norm = epi.norm_w != nullptr;
+  uint8_t* lds_g = smem + KS * 2 * kXBuf;
+  __shared__ float s_rn[64];
   // this thread's x pieces: piece pc = gt + 64 TW u is row pc / 16, bytes 16 (pc % 16) of the chunk; rows >= M read
   // past the end (zeros); in a partial last round, threads past the last piece (xl < 0) load and store nothing
-  int xoff[kPer], xl[kPer];
+  int xoff[kPer], xl[kPer], goff[kPer], xrow[kPer];       // goff: the piece's byte offset in a chunk of lds_g
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int pc = gt + kGroupThreads * u;
     const bool in = kWhole || pc < kPieces;
     xoff[u] = in ? ((pc >> 4) * K + 8 * (pc & 15)) * 2 : kOutOfRange;
     xl[u] = in ? (pc >> 4) * kXPitch + 16 * ((pc & 15) ^ xswz((pc >> 4) & 15)) : -1;
+    goff[u] = 16 * (pc & 15);
+    xrow[u] = in ? pc >> 4 : 0;
   }
   auto piece_live = [&](int u) { return kWhole || u + 1 < kPer || xl[u] >= 0; };
 
@@ -123,15 +132,25 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
 #pragma unroll
     for (int u = 0; u < kPer; ++u) rx[d][u] = buffer_load16(xr, live && piece_live(u) ? xoff[u] + 256 * c : kOutOfRange);
   };
-  auto stage_x = [&](int d, int b) {                        // x pieces of slot d -> LDS buffer b
+  auto stage_x = [&](int d, int b, int step) {              // x pieces of slot d (step) -> LDS buffer b
 #pragma unroll
     for (int u = 0; u < kPer; ++u)
-      if (piece_live(u)) *reinterpret_cast<u32x4*>(xbuf + b * kXBuf + xl[u]) = rx[d][u];
+      if (piece_live(u))
+        *reinterpret_cast<u32x4*>(xbuf + b * kXBuf + xl[u]) =
+            norm && kg + KS * step < ce - cb    // a step past the group's chunks stages its zeros as they are
+                ? rms_apply8(rx[d][u], *reinterpret_cast<const u32x4*>(lds_g + goff[u] + 256 * (kg + KS * step)),
+                             s_rn[xrow[u]])
+                : rx[d][u];
   };
 
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d, d);
-  stage_x(0, 0);
+  if (norm) {                                               // the rows' statistics while the ring is in flight
+    stage_norm_weights(epi.norm_w, cb, ce, lds_g);
+    rms_rows(xr, M, K, 16 * MT, epi.norm_eps, wave, TW * KS, lane, s_rn);
+    __syncthreads();
+  }
+  stage_x(0, 0, 0);
   __syncthreads();
 
   f32x4 acc[RW][MT];
@@ -187,7 +206,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
       const int j = j0 + d;
       consume(d, j & 1);
       issue(d, j + D);
-      if (j + 1 < nsteps) stage_x((d + 1) % D, (j + 1) & 1);
+      if (j + 1 < nsteps) stage_x((d + 1) % D, (j + 1) & 1, j + 1);
       __syncthreads();
     }
   }
@@ -196,7 +215,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
     const int j = j0 + d;
     if (j < nsteps) {
       consume(d, j & 1);
-      if (j + 1 < nsteps) stage_x(d + 1, (j + 1) & 1);
+      if (j + 1 < nsteps) stage_x(d + 1, (j + 1) & 1, j + 1);
       __syncthreads();
     }
   }
@@ -351,6 +370,12 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)t * 8 * K, (uint32_t)(rows * (K / 2)));
   const __amdgpu_buffer_rsrc_t sr = make_rsrc(s, (uint32_t)N * (uint32_t)KG * 2u);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)M * (uint32_t)K * 2u);
+  // the input RMSNorm (epi.norm_w): each B fragment normalized before its MFMA, with its row's 1 / RMS (over all of K)
+  // and the norm weights of its 8 columns (staged in LDS after the reduction scratch, lds_g). Not built for MT = 4,
+  // whose registers it would spill (the launcher sends a normalized 49..64-row input to the row-group kernel).
+  const bool norm = MT <= kTilesNormMaxMT && epi.norm_w != nullptr;
+  uint8_t* lds_g = smem + (size_t)(W - 1) * MT * 64 * 16;
+  __shared__ float s_rn[64];
   const bool wlive = r < rows;
   const int woff = wlive ? 64 * r + 16 * q : 0, wstep = rows * 64;
   const int srow = n0 + 4 * q + (r & 3);
@@ -385,7 +410,8 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   const DecodeRegs dc = decode_regs();
-  auto consume = [&](int d) {
+  float rnr[MT];                                            // 1 / RMS of this lane's B rows (norm)
+  auto consume = [&](int d, int c) {                        // slot d holds chunk c
     f32x4 pt[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) pt[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -393,8 +419,12 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
     for (int j = 0; j < 4; ++j) {
       const f16x8 a = decode_word_a(rw[d][j], dc);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        pt[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, rx[d][mt][j]), pt[mt], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 b =
+            norm ? rms_apply8(rx[d][mt][j], *reinterpret_cast<const u32x4*>(lds_g + 2 * (128 * c + 32 * q + 8 * j)), rnr[mt])
+                 : rx[d][mt][j];
+        pt[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, b), pt[mt], 0, 0, 0);
+      }
     }
     const uint32_t sb = rs[d];
     const float sc[4] = {(float)__builtin_bit_cast(f16, (uint16_t)quad_bcast<0>(sb)),
@@ -412,17 +442,24 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
   const int nj = (KC - wave + W - 1) / W;
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d, d);
+  if (norm) {                                               // the rows' statistics while the ring is in flight
+    stage_norm_weights(epi.norm_w, 0, KC, lds_g);
+    rms_rows(xr, M, K, 16 * MT, epi.norm_eps, wave, W, lane, s_rn);
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) rnr[mt] = s_rn[16 * mt + r];
+  }
   int j0 = 0;
   for (; j0 + D <= nj; j0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      consume(d);
+      consume(d, wave + (j0 + d) * W);
       issue(d, j0 + d + D);
     }
   }
 #pragma unroll
   for (int d = 0; d < D - 1; ++d)
-    if (j0 + d < nj) consume(d);
+    if (j0 + d < nj) consume(d, wave + (j0 + d) * W);
 
   // waves 1 .. W-1 hand their sums to wave 0, which adds them in wave order
   if (W > 1) {
@@ -487,13 +524,17 @@ hipError_t launch_gemm(const GemvArgs& a, const GemvPlan& p, uint32_t* ctr, floa
     return hipErrorInvalidConfiguration;                    // never planned
   } else {
     const int ntiles = (a.N + 15) / 16, groups = (ntiles + TW * RW - 1) / (TW * RW);
+    // x buffers, then (input norm) the norm weights of the longest split's chunks; the K-group sums reuse the space
+    const int KC = a.K / 128;
     const size_t xbytes = (size_t)KS * 2 * 16 * MT * kXPitch, redbytes = (size_t)(KS - 1) * TW * RW * MT * 1024;
-    const size_t shmem = std::max(xbytes, redbytes);
+    const size_t gbytes = a.epi.norm_w ? (size_t)256 * ((KC + p.S - 1) / p.S) : 0;
+    const size_t shmem = std::max(xbytes + gbytes, redbytes);
     // the RoPE epilogue is its own instantiation: its registers would cost every other epilogue occupancy
     auto kern = a.epi.mode == kEpiRopeQKV ? gemm_mfma<MT, RW, D, KS, TW, true> : gemm_mfma<MT, RW, D, KS, TW, false>;
     if (shmem > 65536) {                                     // above the default dynamic LDS limit (gfx950 has 160 KB)
-      static const hipError_t attr[2] = {allow_lds(gemm_mfma<MT, RW, D, KS, TW, false>, shmem),
-                                         allow_lds(gemm_mfma<MT, RW, D, KS, TW, true>, shmem)};
+      // (x buffers at most 128 KB; the norm weights of K <= 8192 at most 16 KB more)
+      static const hipError_t attr[2] = {allow_lds(gemm_mfma<MT, RW, D, KS, TW, false>, kGemmMaxLds),
+                                         allow_lds(gemm_mfma<MT, RW, D, KS, TW, true>, kGemmMaxLds)};
       if (attr[0] != hipSuccess) return attr[0];
       if (attr[1] != hipSuccess) return attr[1];
     }
@@ -546,7 +587,7 @@ template <int MT, int D>
 hipError_t launch_tiles_d(const GemvArgs& a, int waves) {
   constexpr int kThreads = 512;
   if (waves < 1 || 64 * waves > kThreads) return hipErrorInvalidConfiguration;   // never planned
-  const size_t shmem = (size_t)(waves - 1) * MT * 64 * 16;
+  const size_t shmem = (size_t)(waves - 1) * MT * 64 * 16 + (a.epi.norm_w ? (size_t)2 * a.K : 0);   // + norm weights
   auto kern = a.epi.mode == kEpiRopeQKV ? gemm_mfma_tiles<MT, D, kThreads, true> : gemm_mfma_tiles<MT, D, kThreads, false>;
   return launch(kern, dim3((a.N + 15) / 16), dim3(64 * waves), shmem, a.stream, a.x, a.w,
                 a.s, a.y, a.M, a.N, a.K, a.G, a.epi);
@@ -716,8 +757,13 @@ hipError_t zero_words_launch(void* p, int n, hipStream_t stream) {
   return launch(zero_words, dim3(blocks), dim3(256), 0, stream, static_cast<uint32_t*>(p), n);
 }
 
-hipError_t gemm_mfma_launch(const GemvArgs& a, int row_tiles, void* workspace, size_t workspace_bytes) {
-  const GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
+hipError_t gemm_mfma_launch(const GemvArgs& a0, int row_tiles, void* workspace, size_t workspace_bytes) {
+  GemvArgs a = a0;                                          // the input norm travels with the epilogue
+  a.epi.norm_w = a0.norm_w;
+  a.epi.norm_eps = a0.eps;
+  GemvPlan p = plan_gemm_mfma(a.M, a.N, a.K, row_tiles, workspace ? workspace_bytes : 0);
+  if (p.TW > 0 && p.MT > kTilesNormMaxMT && a.norm_w)    // row groups normalize at every M
+    p = plan_gemm_mfma(a.M, a.N, a.K, 1, workspace ? workspace_bytes : 0);
   if (p.TW > 0)
     return p.MT == 1 ? launch_tiles<1>(a, p.TW, p.D) : p.MT == 2 ? launch_tiles<2>(a, p.TW, p.D)
          : p.MT == 3 ? launch_tiles<3>(a, p.TW, p.D) : launch_tiles<4>(a, p.TW, p.D);

@@ -279,13 +279,7 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
       const int b = (int)threadIdx.x + u * (int)blockDim.x;
       if (b < nb) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const f16x2 v = as_f16x2(xst[u][j][e]), g = as_f16x2(wst[u][j][e]);
-            const f16x2 nv = {(f16)((float)v[0] * rn), (f16)((float)v[1] * rn)};
-            xst[u][j][e] = as_u32(f16x2{(f16)((float)g[0] * (float)nv[0]), (f16)((float)g[1] * (float)nv[1])});
-          }
+        for (int j = 0; j < 4; ++j) xst[u][j] = rms_apply8(xst[u][j], wst[u][j], rn);
       }
     }
   }

@@ -34,7 +34,80 @@ struct Epilogue {
   // [head][partition] of kAttnRec floats, attn_parts partitions per head (2 .. kAttnXMaxParts); nullptr: x as given
   const float* attn_part = nullptr;
   int attn_parts = 0;
+  // the MFMA GEMMs (M >= 2): project RMSNorm(x) * norm_w instead of x (lowbit_rmsnorm's arithmetic); nullptr: x
+  const f16* norm_w = nullptr;
+  float norm_eps = 0.f;
 };
+
+// RMSNorm statistics of rows 0 .. rows - 1 of x [M, K] (rows past M get 0) into rn[] (LDS): 1 / sqrt(mean(x^2) + eps),
+// with lowbit_rmsnorm's arithmetic to the bit. That kernel's thread t (of 256) adds the squares of pieces t, t + 256,
+// ... in order, each wave sums its threads with wave_sum and the four wave totals are added in wave order; here lane l
+// keeps the sums of threads l, l + 64, l + 128, l + 192 apart (u = 0..3: pieces l + 64 u + 256 c, c = 0, 1, ...) and
+// adds them the same way. Wave w takes rows 2w, 2w + 1, then 2w + 2W, ... (the loads of a pair of rows, 4 pieces each,
+// requested before the first add; K <= 2048 is one batch). The caller synchronizes before reading rn.
+__device__ __forceinline__ void rms_rows(__amdgpu_buffer_rsrc_t xr, int M, int K, int rows, float eps, int wave,
+                                         int W, int lane, float* rn) {
+  const int np = K >> 3;
+  for (int m0 = 2 * wave; m0 < rows; m0 += 2 * W) {
+    float ss[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int p0 = lane; p0 < np; p0 += 64 * 4) {
+      u32x4 v[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int m = m0 + r, p = p0 + 64 * u;
+          v[r][u] = buffer_load16(xr, m < M && p < np ? (m * K + 8 * p) * 2 : kOutOfRange);
+        }
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {                     // (a piece past the row adds exact zeros)
+            const f16x2 h = as_f16x2(v[r][u][j]);
+            ss[r][u] = fmaf((float)h[0], (float)h[0], ss[r][u]);
+            ss[r][u] = fmaf((float)h[1], (float)h[1], ss[r][u]);
+          }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s += wave_sum(ss[r][u]);
+      const int m = m0 + r;
+      if (lane == 0 && m < rows) rn[m] = m < M ? rsqrtf(s / (float)K + eps) : 0.f;
+    }
+  }
+}
+
+// the norm weights of 128-k chunks c0 .. c1 - 1 into LDS at g (16-byte pieces round robin over the workgroup)
+__device__ __forceinline__ void stage_norm_weights(const f16* w, int c0, int c1, uint8_t* g) {
+  const u32x4* src = reinterpret_cast<const u32x4*>(w) + 16 * c0;
+  for (int p = threadIdx.x; p < 16 * (c1 - c0); p += blockDim.x) reinterpret_cast<u32x4*>(g)[p] = src[p];
+}
+
+// fp16 of an fp32 value that the compiler must hold in fp32 first: hipcc otherwise may fuse the product that made it
+// and this conversion into one mixed-precision multiply-add (v_fma_mixlo_f16), rounding once instead of twice, which
+// differs in rare cases (an fp32 product that lands on an fp16 rounding midpoint)
+__device__ __forceinline__ f16 f16_of_f32(float a) {
+  asm("" : "+v"(a));
+  return (f16)a;
+}
+
+// eight values of a row normalized as torch's fp16 RMSNorm (transformers' Qwen2RMSNorm) writes them: fp16 of the
+// fp32 product x r, then fp16 of w times that (exact in fp32, so one rounding). lowbit_rmsnorm, the GEMV's and the
+// MFMA GEMMs' input norm all normalize with this function.
+__device__ __forceinline__ u32x4 rms_apply8(const u32x4& v, const u32x4& g, float r) {
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f16x2 p = as_f16x2(v[j]), w = as_f16x2(g[j]);
+    const f16x2 n = {f16_of_f32((float)p[0] * r), f16_of_f32((float)p[1] * r)};
+    o[j] = as_u32(f16x2{(f16)((float)w[0] * (float)n[0]), (f16)((float)w[1] * (float)n[1])});
+  }
+  return o;
+}
 
 // Four outputs of the kEpiRopeQKV epilogue, packed fp16, and where they go (dst == nullptr: nothing to store): dims
 // d .. d + 3 of a head in `lo`, their partners d + 64 .. d + 67 in `hi`, stored 64 values on.

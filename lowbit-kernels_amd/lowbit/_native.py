@@ -48,7 +48,7 @@ SIGNATURES = {
                             _i64, _i64, _vp], _int),
     "lowbit_rope_table": ([_vp, _vp, _vp, _i64, _vp], _int),
     "lowbit_w4_qkv_rope_rows": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
-                                 _i64, _vp, ctypes.c_size_t, _vp], _int),
+                                 _i64, _vp, ctypes.c_float, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
@@ -337,7 +337,8 @@ class NativeExt:
     def w4_linear_fused(self, x, w, s, group, epilogue, aux=None, out=None, norm=None):
         """x [M, K] (M <= 64) times the MFMA-layout weight with the epilogue fused into the store; returns y
         ([M, N], or [M, N / 2] for EPI_SILU_MUL). `out` may be given (for EPI_RESIDUAL it may be `aux` itself).
-        norm = (weight, eps), M = 1 only: project RMSNorm(x) * weight instead of x."""
+        norm = (weight, eps): project RMSNorm(x) * weight instead of x, normalized in the kernel with lowbit_rmsnorm's
+        bits (K <= 16384 for one row, K <= 8192 for 2..64)."""
         import torch
         _check_tensors(x, w, s, group)
         m, n = x.shape[0], w.shape[0]
@@ -442,13 +443,16 @@ class NativeExt:
             check(self.lib.lowbit_rope_table(ptr(positions), ptr(inv_freq), ptr(t), m, _stream(positions.device)))
         return t
 
-    def w4_qkv_rope_rows(self, x, w, s, group, bias, positions, table, q_out, k_cache, v_cache, hq, hkv):
-        """M tokens: the RoPE-permuted q|k|v projection of the normalized input x [M, K] (+ bias, RoPE, cache write)
-        into q_out [M, Hq, 128] and the caches [Hkv, L, 128] at rows positions[m]; table = rope_table(positions, ...)
-        (the MFMA GEMM up to 64 rows, the prefill GEMM beyond, each with its own workspace)."""
+    def w4_qkv_rope_rows(self, x, w, s, group, bias, positions, table, q_out, k_cache, v_cache, hq, hkv, norm=None):
+        """M tokens: the RoPE-permuted q|k|v projection of the input x [M, K] (+ bias, RoPE, cache write) into q_out
+        [M, Hq, 128] and the caches [Hkv, L, 128] at rows positions[m]; table = rope_table(positions, ...) (the MFMA
+        GEMM up to 64 rows, the prefill GEMM beyond, each with its own workspace). norm = (weight, eps), up to 64 rows and
+        K <= 8192: project RMSNorm(x) * weight, normalized in the GEMM (lowbit_rmsnorm's bits); otherwise x is the
+        normalized input."""
         import torch
         _check_tensors(x, w, s, group)
         m = x.shape[0]
+        _check_norm(norm, x.shape[1], x.device)
         if w.shape[0] != (hq + 2 * hkv) * 128:
             raise RuntimeError("the q|k|v weight must have (Hq + 2 Hkv) * 128 rows")
         _need(bias, "bias", torch.float16, (w.shape[0],), x.device)
@@ -462,9 +466,11 @@ class NativeExt:
         with _DeviceGuard(x.device):
             st = _stream(x.device)
             ws = workspace(x.device, st, WORKSPACE_BYTES if m <= 64 else PREFILL_WORKSPACE_BYTES)
+            nw, eps = norm if norm is not None else (None, 0.0)
             check(self.lib.lowbit_w4_qkv_rope_rows(ptr(x), ptr(w), ptr(s), m, w.shape[0], x.shape[1], group, ptr(bias),
                                                    ptr(positions), ptr(table), ptr(q_out), ptr(k_cache), ptr(v_cache),
-                                                   hq, hkv, k_cache.shape[1], ptr(ws), ws.numel(), st))
+                                                   hq, hkv, k_cache.shape[1], ptr(nw) if nw is not None else None,
+                                                   float(eps), ptr(ws), ws.numel(), st))
 
     def attention(self, q, k_cache, v_cache, positions, out, hq, hkv, max_keys, scale, split=True):
         """split=False runs one block per (token, head group), without the key partitions and their workspace."""

@@ -47,6 +47,14 @@ def rope_permutation(heads, head_dim=128):
     return torch.tensor([h * head_dim + d for h in range(heads) for d in within], dtype=torch.long)
 
 
+# Rows up to which a projection takes its input norm fused (norm_weight of lowbit_w4_linear_fused and
+# lowbit_w4_qkv_rope_rows) rather than after a separate lowbit_rmsnorm launch. Every workgroup of the MFMA GEMM reads
+# the rows whole for their statistics: up to 16 rows that costs less than the launch it saves, beyond it more (MI355X,
+# graph-timed, cold weights: 3B gate|up 11.0 us fused against 11.3 for rmsnorm + GEMM at 16 rows, 16.9 against 14.5 at
+# 48; 3B decode feeding 16 tokens a step 7980 -> 8250 tokens/s, 48 a step 19170 -> 18350 had it been fused there too).
+FUSED_NORM_ROWS = 16
+
+
 class _W4:
     """A merged W4A16 projection: W4Weight on the MFMA layout plus its bias."""
 
@@ -56,8 +64,11 @@ class _W4:
 
     def __call__(self, x, epilogue, aux=None, out=None, norm=None):
         wq = self.wq
-        if x.shape[0] <= 64:
+        if x.shape[0] <= 64:                                 # the GEMV / MFMA GEMM, the input norm in its prologue
+            if norm is not None and (x.shape[0] > FUSED_NORM_ROWS or x.shape[1] > (16384 if x.shape[0] == 1 else 8192)):
+                x, norm = _normed(x, norm), None
             return ops.ext().w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out, norm)
+        x = _normed(x, norm)
         if ops.prefill_path(x.shape[0], wq):                 # the int4 prefill GEMM, epilogue fused
             return ops.ext().w4_gemm_prefill(x, wq.packed_mma, wq.scales, wq.group, epilogue, aux, out)
         w = ops.dequant(wq)                                  # prefill: dequantize + hipBLASLt, epilogue in torch
@@ -71,7 +82,7 @@ class _F16:
         self.w, self.bias = weight, bias
 
     def __call__(self, x, epilogue, aux=None, out=None, norm=None):
-        return _torch_epilogue(x, self.w, epilogue, aux, out)
+        return _torch_epilogue(_normed(x, norm), self.w, epilogue, aux, out)
 
 
 class _F16GEMV:
@@ -84,7 +95,12 @@ class _F16GEMV:
     def __call__(self, x, epilogue, aux=None, out=None, norm=None):
         if x.shape[0] == 1 and self.w.shape[1] <= 16384:
             return ops.ext().f16_linear_fused(x, self.w, epilogue, aux, out, norm)
-        return _torch_epilogue(x, self.w, epilogue, aux, out)
+        return _torch_epilogue(_normed(x, norm), self.w, epilogue, aux, out)
+
+
+def _normed(x, norm):
+    """x, or lowbit_rmsnorm(x) * weight for norm = (weight, eps), for the routes without a fused input norm."""
+    return x if norm is None else ops.ext().rmsnorm(x, norm[0], norm[1])
 
 
 def _torch_epilogue(x, w, epilogue, aux, out, round_first=False):
@@ -200,10 +216,15 @@ class FusedQwen2:
                 ext.w4_qkv_rope(h, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, self.inv_freq, q,
                                 self.k_cache[i], self.v_cache[i], self.hq, self.hkv, norm=(lay["in_norm"], self.eps))
             elif rope_rows:                                   # RoPE + cache write in the GEMM's store
-                ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
                 wq = lay["qkv"].wq
-                ext.w4_qkv_rope_rows(xn, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, table, q,
-                                     self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
+                if m <= FUSED_NORM_ROWS and self.hidden <= 8192:   # the MFMA GEMM normalizes its input itself
+                    ext.w4_qkv_rope_rows(h, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, table, q,
+                                         self.k_cache[i], self.v_cache[i], self.hq, self.hkv,
+                                         norm=(lay["in_norm"], self.eps))
+                else:
+                    ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
+                    ext.w4_qkv_rope_rows(xn, wq.packed_mma, wq.scales, wq.group, lay["qkv"].bias, positions, table,
+                                         q, self.k_cache[i], self.v_cache[i], self.hq, self.hkv)
             else:
                 ext.rmsnorm(h, lay["in_norm"], self.eps, out=xn)
                 qkv = lay["qkv"](xn, EPI_BIAS, lay["qkv"].bias)
@@ -222,7 +243,7 @@ class FusedQwen2:
                 ext.attention(q, self.k_cache[i], self.v_cache[i], positions, attn, self.hq, self.hkv, self.max_len,
                               self.scale)
                 lay["o"](attn, EPI_RESIDUAL, h, out=h)
-            if fuse:
+            if fuse or (self.quant == "int4" and m <= FUSED_NORM_ROWS and self.hidden <= 8192):   # normalized in the GEMM
                 act = lay["gu"](h, EPI_SILU_MUL, norm=(lay["post_norm"], self.eps))
             else:
                 ext.rmsnorm(h, lay["post_norm"], self.eps, out=xn)

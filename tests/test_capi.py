@@ -71,20 +71,22 @@ def _msg(rc):
     (lambda l: l.lowbit_set_gemm_tile_waves(2), 8, "tile_waves is 0"),
     (lambda l: l.lowbit_set_gemm_tile_waves(7), 8, "tile_waves is 0"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 0, 512, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
-                                         64, None, 0, None), 5, "at least one row"),
+                                         64, None, ctypes.c_float(0), None, 0, None), 5, "at least one row"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 640, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
-                                         64, None, 0, None), 3, "(Hq + 2 Hkv) * 128"),
+                                         64, None, ctypes.c_float(0), None, 0, None), 3, "(Hq + 2 Hkv) * 128"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 512, 128, 128, None, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
-                                         64, None, 0, None), 1, "null pointer"),
+                                         64, None, ctypes.c_float(0), None, 0, None), 1, "null pointer"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 100, 512, 1 << 23, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
-                                         2, 1, 64, None, 0, None), 3, "K is at most"),
+                                         2, 1, 64, None, ctypes.c_float(0), None, 0, None), 3, "K is at most"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 512, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
-                                         64, FAKE, 4096, None), 1, "workspace"),
+                                         64, None, ctypes.c_float(0), FAKE, 4096, None), 1, "workspace"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 512, 128, 128, FAKE, FAKE, ctypes.c_void_p(4104), FAKE,
-                                         FAKE, FAKE, 2, 1, 64, None, 0, None), 4, "16-byte aligned rope table"),
+                                         FAKE, FAKE, 2, 1, 64, None, ctypes.c_float(0), None, 0, None), 4, "16-byte aligned rope table"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 512, 128, 128, FAKE, FAKE, FAKE, FAKE,
-                                         ctypes.c_void_p(4098), FAKE, 2, 1, 64, None, 0, None), 4, "8-byte aligned"),
-    (lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
+                                         ctypes.c_void_p(4098), FAKE, 2, 1, 64, None, ctypes.c_float(0), None, 0, None), 4, "8-byte aligned"),
+        (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 100, 512, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
+                                         64, FAKE, ctypes.c_float(1e-6), None, 0, None), 1, "at most 64 rows"),
+(lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, FAKE, 0, None), 3, "M must be positive"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, ctypes.c_void_p(4098), 4, None), 4, "4-byte aligned"),
     (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,

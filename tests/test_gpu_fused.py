@@ -63,8 +63,45 @@ def test_fused_input_norm_matches_norm_then_projection(cuda, k, n):
             want = ext.w4_linear_fused(ext.rmsnorm(x, nw, 1e-6), wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL)
             got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL, norm=(nw, 1e-6))
             assert rel(got, want.double()) < 2e-3, (k, n, scale)
-    with pytest.raises(RuntimeError, match="one row"):
-        x2 = torch.randn(2, k, generator=gen).half().cuda()
+
+
+@pytest.mark.parametrize("k,n", [(1536, 2048), (2048, 22016), (2048, 2560), (3584, 512), (256, 4096)])
+def test_fused_input_norm_on_the_mfma_gemm(cuda, k, n):
+    """2 to 64 rows: the MFMA GEMM normalizes its input in its prologue (each row's sum of squares added in
+    lowbit_rmsnorm's order, then its two fp16 roundings as the pieces are staged or the fragments built) -- on the
+    one-tile and the row-group kernels, with and without a K split -- the same bits as lowbit_rmsnorm followed by the
+    same GEMM, rows of very different scale in one call."""
+    wq, _, *_, gen = make_weight(k, n, 7 * k + n, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    nw = (1 + 0.1 * torch.randn(k, generator=gen)).half().cuda()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    lib = _native.lib()
+    try:
+        for m in (2, 16, 17, 33, 48, 64):
+            rows = torch.randn(m, k, generator=gen) * torch.logspace(-3, 1.6, m).view(m, 1)
+            x = rows.half().cuda()
+            for kern in (0, 1, 2):
+                # the one-tile kernel normalizes up to 48 rows; a normalized input of more goes to row groups (the
+                # plan of kernel 1 and the automatic one's when it takes row groups)
+                _native.check(lib.lowbit_set_gemm_kernel(1 if m > 48 else kern))
+                xn = ext.rmsnorm(x, nw, 1e-6)
+                want = ext.w4_linear_fused(xn, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias)
+                want_sm = ext.w4_linear_fused(xn, wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL) \
+                    if n % 16 == 0 else None
+                _native.check(lib.lowbit_set_gemm_kernel(kern))
+                got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias, norm=(nw, 1e-6))
+                assert torch.equal(got, want), (k, n, m, kern)
+                if want_sm is not None:
+                    got = ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_SILU_MUL,
+                                              norm=(nw, 1e-6))
+                    assert torch.equal(got, want_sm), (k, n, m, kern)
+                assert torch.equal(ext.w4_linear_fused(x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias,
+                                                       norm=(nw, 1e-6)), ext.w4_linear_fused(
+                    x, wq.packed_mma, wq.scales, wq.group, fused.EPI_BIAS, bias, norm=(nw, 1e-6)))
+    finally:
+        _native.check(lib.lowbit_set_gemm_kernel(0))
+    with pytest.raises(RuntimeError):                          # the prefill GEMM has no fused norm
+        x2 = torch.randn(65, k, generator=gen).half().cuda()
         ext.w4_linear_fused(x2, wq.packed_mma, wq.scales, wq.group, fused.EPI_STORE, norm=(nw, 1e-6))
 
 
@@ -244,6 +281,41 @@ def test_qkv_rope_rows_equal_projection_then_rope(cuda, hq, hkv, k, m):
         written[pos[pos < L]] = True
         assert int(torch.count_nonzero(outs[1][1][:, ~written])) == 0
         assert int(torch.count_nonzero(outs[1][1][:, written])) > outs[1][1][:, written].numel() * 0.99
+
+
+@pytest.mark.parametrize("hq,hkv,k,m", [(16, 2, 2048, 16), (16, 2, 2048, 48), (12, 2, 1536, 33), (2, 1, 256, 5)])
+def test_qkv_rope_rows_with_the_input_norm(cuda, hq, hkv, k, m):
+    """lowbit_w4_qkv_rope_rows with norm_weight (up to 64 rows: the MFMA GEMM normalizes x itself) against
+    lowbit_rmsnorm followed by the same call: the same q and cache rows, bit for bit."""
+    n, L = (hq + 2 * hkv) * 128, 300
+    wq, _, *_, gen = make_weight(k, n, 5 * k + n + m, layouts=("mma",), sd=0.05)
+    ext = ops.ext()
+    bias = (torch.randn(n, generator=gen) * 0.5).half().cuda()
+    nw = (1 + 0.1 * torch.randn(k, generator=gen)).half().cuda()
+    inv_freq = (1.0 / (1e6 ** (torch.arange(0, 128, 2, dtype=torch.float32) / 128))).cuda()
+    x = (torch.randn(m, k, generator=gen) * 7).half().cuda()
+    pos = torch.randperm(L, generator=gen)[:m].cuda()
+    table = ext.rope_table(pos, inv_freq)
+    outs = []
+    for fused_norm in (False, True):
+        q = torch.zeros(m, hq, 128, dtype=torch.half, device="cuda")
+        kc = torch.zeros(hkv, L, 128, dtype=torch.half, device="cuda")
+        vc = torch.zeros_like(kc)
+        if fused_norm:
+            ext.w4_qkv_rope_rows(x, wq.packed_mma, wq.scales, wq.group, bias, pos, table, q, kc, vc, hq, hkv,
+                                 norm=(nw, 1e-6))
+        else:
+            ext.w4_qkv_rope_rows(ext.rmsnorm(x, nw, 1e-6), wq.packed_mma, wq.scales, wq.group, bias, pos, table, q, kc,
+                                 vc, hq, hkv)
+        outs.append((q, kc[:, pos], vc[:, pos]))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b), m
+    with pytest.raises(RuntimeError, match="at most 64 rows"):
+        x2 = torch.randn(65, k, generator=gen).half().cuda()
+        pos2 = torch.arange(65, device="cuda")
+        ext.w4_qkv_rope_rows(x2, wq.packed_mma, wq.scales, wq.group, bias, pos2, ext.rope_table(pos2, inv_freq),
+                             torch.zeros(65, hq, 128, dtype=torch.half, device="cuda"), kc, vc, hq, hkv,
+                             norm=(nw, 1e-6))
 
 
 @pytest.mark.parametrize("hq,hkv,L,positions", [(16, 2, 1100, [0]), (16, 2, 1100, [767]), (12, 2, 600, [63, 64, 65]),
