@@ -166,7 +166,9 @@ int lowbit_w4_relayout(const void* src, void* dst, int64_t N, int64_t K, int lay
  * (nn.Linear bias add of the reference's W4Linear, lowbit/model.py:25-26; the residual add and silu(gate) * up of
  * transformers' Qwen2 layer). norm_weight (may be NULL; 16-byte aligned; K <= 16384 at M = 1, K <= 8192 at M >= 2): project
  * lowbit_rmsnorm(x, norm_weight, eps) instead of x, the norm computed in the kernel's prologue with lowbit_rmsnorm's
- * arithmetic (the same bits as lowbit_rmsnorm followed by the projection). */
+ * per-element arithmetic; for 2..64 rows each row's sum of squares is also added in lowbit_rmsnorm's order (the same
+ * bits as lowbit_rmsnorm followed by the projection), for one row in the GEMV's own order (1 / RMS may differ from
+ * lowbit_rmsnorm's in its last bit). */
 int lowbit_w4_linear_fused(const void* x, const void* w, const void* s, void* y, int64_t M, int64_t N, int64_t K,
                            int64_t group, int epilogue, const void* aux, const void* norm_weight, float eps,
                            void* workspace, size_t workspace_bytes, void* stream);

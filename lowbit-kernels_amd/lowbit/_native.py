@@ -337,8 +337,8 @@ class NativeExt:
     def w4_linear_fused(self, x, w, s, group, epilogue, aux=None, out=None, norm=None):
         """x [M, K] (M <= 64) times the MFMA-layout weight with the epilogue fused into the store; returns y
         ([M, N], or [M, N / 2] for EPI_SILU_MUL). `out` may be given (for EPI_RESIDUAL it may be `aux` itself).
-        norm = (weight, eps): project RMSNorm(x) * weight instead of x, normalized in the kernel with lowbit_rmsnorm's
-        bits (K <= 16384 for one row, K <= 8192 for 2..64)."""
+        norm = (weight, eps): project RMSNorm(x) * weight instead of x, normalized in the kernel (K <= 16384 for one
+        row; K <= 8192 for 2..64 rows, with lowbit_rmsnorm's bits)."""
         import torch
         _check_tensors(x, w, s, group)
         m, n = x.shape[0], w.shape[0]
