@@ -38,8 +38,14 @@ __device__ __forceinline__ int swz(int row, int blk) { return row * 16 + (blk ^ 
 
 }  // namespace
 
+// Waves per SIMD the register allocation must leave room for: 2 for the 4-tile, 2-slot shapes (at most 256 registers
+// a wave, so two 4-wave workgroups share a CU), which fit in that budget without spilling; 1 for the 8-tile and 3-slot
+// shapes, which do not. Without the bound hipcc gave the 4 x 4-tile shape 260 registers (188 + 72 accumulation
+// registers): one workgroup per CU, and 3B gate|up at 2048 rows took 455 us instead of 249 (MI355X, cold weights).
+constexpr int prefill_min_waves(int MT, int D) { return MT == 4 && D == 2 ? 2 : 1; }
+
 template <int MT, int D, int NW, int XL, int PT, bool ROPE>
-__global__ __launch_bounds__(64 * NW) void gemm_prefill(const f16* __restrict__ x, const uint8_t* __restrict__ w,
+__global__ __launch_bounds__(64 * NW, prefill_min_waves(MT, D)) void gemm_prefill(const f16* __restrict__ x, const uint8_t* __restrict__ w,
                                                     const f16* __restrict__ s, f16* y, int M, int N, int K, int G,
                                                     int S, int MG, int items, uint32_t* __restrict__ ctr,
                                                     float* __restrict__ part, Epilogue epi) {
