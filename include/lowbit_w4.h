@@ -282,6 +282,15 @@ int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* 
  * in the fused decoder, where hipBLASLt streams the 622 MB Qwen2.5-3B head at ~3 TB/s. */
 int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* lowbit_f16_gemv for one row followed by the greedy pick and its feedback (replaces the reference harness's
+ * lg.argmax(-1) and the copy that feeds the pick back as the next step's input, bench/e2e.py:93-95): y [1, N] as
+ * lowbit_f16_gemv writes it, then tokens[0] = the index of the largest of y as torch.argmax picks it (the first of
+ * equal maxima, -0 equal to +0, a NaN above every number) and positions[0] += 1 (positions may be NULL). Two launches,
+ * no allocation and no memset, so a decode step may capture it; workspace (8-byte aligned) holds a 64-bit key per
+ * head workgroup, 8 * ceil(N / 8) bytes, and needs no initial contents. */
+int lowbit_f16_gemv_pick(const void* x, const void* w, void* y, int64_t N, int64_t K, void* workspace,
+                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, void* stream);
+
 /* ---- HBM bandwidth probes (the measured peak that kernel bandwidths are quoted against) ----
  * The reference measures its peak with a torch device copy and a torch sum over 256 MiB (bench/gpu_run.py:133-141);
  * these are streaming kernels of this library for the same two figures. hbm_read reads `bytes` (a multiple of 16,

@@ -595,6 +595,26 @@ int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N,
                     "f16_gemv");
 }
 
+int lowbit_f16_gemv_pick(const void* x, const void* w, void* y, int64_t N, int64_t K, void* workspace,
+                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, void* stream) {
+  if (!x || !w || !y || !workspace || !tokens) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (N < 1 || K < 8 || K % 8 || !fits_int(N) || K * 2 > 65536)
+    return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 8 == 0 and K * 2 <= 65536");
+  if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(workspace) | reinterpret_cast<uintptr_t>(tokens) |
+       reinterpret_cast<uintptr_t>(positions)) & 7)
+    return fail(LOWBIT_ERR_ALIGN, "f16_gemv_pick needs an 8-byte aligned workspace, tokens and positions");
+  const size_t need = (size_t)8 * head_pick_parts((int)N);
+  if (workspace_bytes < need)
+    return fail(LOWBIT_ERR_ARG, "f16_gemv_pick needs a workspace of at least %zu bytes for N = %lld", need,
+                (long long)N);
+  if (int rc = check_device()) return rc;
+  return hip_status(head_pick_launch(static_cast<const f16*>(x), static_cast<const f16*>(w), static_cast<f16*>(y),
+                                     (int)N, (int)K, static_cast<uint64_t*>(workspace), tokens, positions,
+                                     static_cast<hipStream_t>(stream)),
+                    "f16_gemv_pick");
+}
+
 int lowbit_hbm_read(const void* src, int64_t bytes, void* sink, int64_t blocks, void* stream) {
   if (!src || !sink) return fail(LOWBIT_ERR_ARG, "null pointer argument");
   if (bytes < 16 || bytes % 16) return fail(LOWBIT_ERR_SHAPE, "hbm_read: bytes must be a positive multiple of 16");

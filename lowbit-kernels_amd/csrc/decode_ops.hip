@@ -424,9 +424,26 @@ __global__ __launch_bounds__(64) void attention_mfma(const f16* __restrict__ q, 
 // row. Two rows per wave, four chunks each (MI355X graph, 3 cold copies of the 151936 x 2048 Qwen2.5 head): 94.3 us
 // (6.6 TB/s) against 102.3 for 8 rows and two chunks, 99.0 for 4 and two, 96.2 for one row and four; same bits.
 constexpr int kHeadChunks = 4;
-template <int M, int RW>
+
+// The greedy pick's order on (fp16 logit, index) as one 64-bit key, larger = picked, as torch.argmax picks: the larger
+// value (-0 equal to +0, a NaN above every number), then the smaller index. Zero is below every key.
+__device__ __forceinline__ uint64_t pick_key(uint16_t b, int idx) {
+  uint32_t k;
+  if ((b & 0x7FFFu) > 0x7C00u) {
+    k = 0x10000u;                                            // NaN
+  } else {
+    if (b == 0x8000u) b = 0;                                 // -0 ties with +0
+    k = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);      // fp16 order as unsigned order
+  }
+  return ((uint64_t)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// PICK (M = 1): each workgroup also writes the key of its largest logit (as stored, fp16) to pick[blockIdx.x], for
+// head_pick_kernel
+template <int M, int RW, bool PICK = false>
 __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                                       f16* __restrict__ y, int N, int K) {
+                                                       f16* __restrict__ y, int N, int K, uint64_t* __restrict__ pick) {
+  static_assert(!PICK || M == 1, "the greedy pick takes one row");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
   // wave through readfirstlane: the row buffer resource below is then known uniform and stays in scalar registers
@@ -436,8 +453,9 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
   for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
   __syncthreads();
   const int n0 = (blockIdx.x * 4 + wave) * RW;
-  if (n0 >= N) return;
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)n0 * K, (uint32_t)(min(RW, N - n0) * K * 2));
+  if (!PICK && n0 >= N) return;                             // (PICK: every wave reaches the barrier below; one past N
+                                                             // reads nothing and stores nothing)
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)min(n0, N) * K, (uint32_t)(max(0, min(RW, N - n0)) * K * 2));
   float acc[RW][M];
 #pragma unroll
   for (int r = 0; r < RW; ++r)
@@ -466,25 +484,84 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
       }
     }
   }
+  uint64_t best = 0;
 #pragma unroll
   for (int r = 0; r < RW; ++r)
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const float v = wave_sum(acc[r][m]);
-      if (lane == 0 && n0 + r < N) y[(size_t)m * N + n0 + r] = (f16)v;
+      if (lane == 0 && n0 + r < N) {
+        const f16 h = (f16)v;
+        y[(size_t)m * N + n0 + r] = h;
+        if constexpr (PICK) {
+          const uint64_t kv = pick_key(__builtin_bit_cast(uint16_t, h), n0 + r);
+          best = kv > best ? kv : best;
+        }
+      }
     }
+  if constexpr (PICK) {
+    __shared__ uint64_t red[4];
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+      for (int v = 1; v < 4; ++v) best = red[v] > best ? red[v] : best;
+      pick[blockIdx.x] = best;
+    }
+  }
 }
 
+// The greedy pick and its feedback, one workgroup: the largest of the head workgroups' keys (pick[0 .. n)) gives the
+// index; tokens[0] = index, positions[0] += 1 (positions may be null)
+constexpr int kPickThreads = 1024;
+__global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t* __restrict__ pick, int n,
+                                                                 int64_t* tokens, int64_t* positions) {
+  __shared__ uint64_t red[kPickThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t best = 0;
+  for (int i0 = tid; i0 < n; i0 += 8 * kPickThreads) {      // eight loads in flight per thread
+    uint64_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = i0 + u * kPickThreads < n ? pick[i0 + u * kPickThreads] : 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) best = v[u] > best ? v[u] : best;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = __shfl_xor(best, off, 64);
+    best = o > best ? o : best;
+  }
+  if (lane == 0) red[wave] = best;
+  __syncthreads();
+  if (tid != 0) return;
+  for (int v = 1; v < kPickThreads / 64; ++v) best = red[v] > best ? red[v] : best;
+  tokens[0] = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
+  if (positions) positions[0] += 1;
+}
+
+constexpr int kHeadRows = 2;                                // RW: rows per wave (4 waves a workgroup)
+
 hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st) {
-  constexpr int RW = 2;
+  constexpr int RW = kHeadRows;
   const dim3 grid((unsigned)((N + 4 * RW - 1) / (4 * RW))), block(256);
   const size_t lds = (size_t)M * K * 2;
   switch (M) {
-    case 1: return launch(gemv_f16_kernel<1, RW>, grid, block, lds, st, x, w, y, N, K);
-    case 2: return launch(gemv_f16_kernel<2, RW>, grid, block, lds, st, x, w, y, N, K);
-    case 3: return launch(gemv_f16_kernel<3, RW>, grid, block, lds, st, x, w, y, N, K);
-    default: return launch(gemv_f16_kernel<4, RW>, grid, block, lds, st, x, w, y, N, K);
+    case 1: return launch(gemv_f16_kernel<1, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
+    case 2: return launch(gemv_f16_kernel<2, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
+    case 3: return launch(gemv_f16_kernel<3, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
+    default: return launch(gemv_f16_kernel<4, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
   }
+}
+
+int head_pick_parts(int N) { return (N + 4 * kHeadRows - 1) / (4 * kHeadRows); }
+
+hipError_t head_pick_launch(const f16* x, const f16* w, f16* y, int N, int K, uint64_t* pick, int64_t* tokens,
+                            int64_t* positions, hipStream_t st) {
+  const int parts = head_pick_parts(N);
+  if (hipError_t e = launch(gemv_f16_kernel<1, kHeadRows, true>, dim3(parts), dim3(256), (size_t)K * 2, st, x, w, y, N,
+                            K, pick))
+    return e;
+  return launch(head_pick_kernel, dim3(1), dim3(kPickThreads), 0, st, pick, parts, tokens, positions);
 }
 
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st) {

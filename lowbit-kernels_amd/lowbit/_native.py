@@ -52,6 +52,7 @@ SIGNATURES = {
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
+    "lowbit_f16_gemv_pick": ([_vp, _vp, _vp, _i64, _i64, _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),
     "lowbit_w4_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _i64,
                                     _i64, _int, _vp, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_f16_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _i64, _int,
@@ -153,6 +154,7 @@ WORKSPACE_COUNTER_BYTES = 16384
 WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (16 << 20)     # LOWBIT_WORKSPACE_BYTES
 PREFILL_WORKSPACE_BYTES = WORKSPACE_COUNTER_BYTES + (64 << 20)
 ATTENTION_WORKSPACE_BYTES = 4 << 20
+PICK_WORKSPACE_BYTES = 1 << 20          # the greedy pick's keys: 8 bytes per 8 head rows
 _WORKSPACES = {}
 _CAPTURE_STREAMS = {}
 
@@ -171,12 +173,13 @@ def capture_stream(device):
     return s
 
 
-def workspace(device, stream, nbytes=WORKSPACE_BYTES):
+def workspace(device, stream, nbytes=WORKSPACE_BYTES, tag=""):
     """A GEMM workspace of `nbytes` for (device, stream): zeroed once, kept for the life of the process (a graph
     captured on the stream keeps using it), so calls on one stream never race on it and never reallocate it. The
-    skinny GEMM and the prefill GEMM each have their own (WORKSPACE_BYTES, PREFILL_WORKSPACE_BYTES)."""
+    skinny GEMM and the prefill GEMM each have their own (WORKSPACE_BYTES, PREFILL_WORKSPACE_BYTES); `tag` keeps a
+    buffer of another kind apart from them whatever its size."""
     import torch
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes, tag)
     ws = _WORKSPACES.get(key)
     if ws is None:
         ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
@@ -552,6 +555,31 @@ class NativeExt:
         with _DeviceGuard(x.device):
             check(self.lib.lowbit_f16_gemv(ptr(x), ptr(w), ptr(y), x.shape[0], w.shape[0], x.shape[1],
                                            _stream(x.device)))
+        return y
+
+    def f16_gemv_pick(self, x, w, tokens, positions=None, out=None):
+        """f16_gemv for one row, then the greedy pick on the GPU: tokens[0] = argmax of the logits (torch.argmax's
+        choice among equal maxima and NaNs), positions[0] += 1 (int64, or None); returns the logits [1, N]."""
+        import torch
+        if x.dim() != 2 or x.shape[0] != 1:
+            raise RuntimeError("f16_gemv_pick takes one row x [1, K]")
+        if not (x.is_cuda and w.is_cuda and x.device == w.device):
+            raise RuntimeError("x and w must be on the same GPU")
+        if x.dtype != torch.float16 or w.dtype != torch.float16 or not (x.is_contiguous() and w.is_contiguous()):
+            raise RuntimeError("x and w must be contiguous float16")
+        if w.dim() != 2 or x.shape[1] != w.shape[1]:
+            raise RuntimeError("x [1, K] and w [N, K]")
+        for name, t in (("tokens", tokens), ("positions", positions)):   # element 0 is written
+            if t is not None and (t.dtype != torch.int64 or not t.is_contiguous() or t.device != x.device or t.numel() < 1):
+                raise RuntimeError(f"{name} must be a contiguous int64 tensor of at least one element on {x.device}")
+        n = w.shape[0]
+        y = out if out is not None else torch.empty((1, n), dtype=torch.float16, device=x.device)
+        _need(y, "out", torch.float16, (1, n), x.device)
+        with _DeviceGuard(x.device):
+            st = _stream(x.device)
+            ws = workspace(x.device, st, max(PICK_WORKSPACE_BYTES, 8 * (-(-n // 8))), tag="pick")
+            check(self.lib.lowbit_f16_gemv_pick(ptr(x), ptr(w), ptr(y), n, x.shape[1], ptr(ws), ws.numel(), ptr(tokens),
+                                                ptr(positions) if positions is not None else None, st))
         return y
 
     def _check_f16_weight(self, x, w):

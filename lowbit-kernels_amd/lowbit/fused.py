@@ -183,17 +183,24 @@ class FusedQwen2:
         self.k_cache.zero_()
         self.v_cache.zero_()
 
-    def logits(self, xn):
+    def head_picks(self):
+        """True when a one-row step's head can take the greedy pick along (lowbit_f16_gemv_pick)."""
+        return self.hidden * 2 <= 65536
+
+    def logits(self, xn, pick=None):
         """The tied fp16 head: the library's fp16 GEMV for up to 4 rows (a bandwidth kernel; hipBLASLt streams the
-        head at ~3 TB/s at these shapes), hipBLASLt beyond."""
+        head at ~3 TB/s at these shapes), hipBLASLt beyond. pick = (tokens, positions), one row (head_picks()): the
+        GEMV also writes the greedy pick to tokens[0] and advances positions[0]."""
+        if pick is not None:
+            return ops.ext().f16_gemv_pick(xn, self.head, pick[0], pick[1])
         if xn.shape[0] <= 4 and xn.shape[1] * xn.shape[0] * 2 <= 65536:
             return ops.ext().f16_gemv(xn, self.head)
         return F.linear(xn, self.head)
 
     @torch.inference_mode()
-    def forward(self, tokens, positions, last_only=False):
+    def forward(self, tokens, positions, last_only=False, pick=None):
         """tokens, positions: int64 [M] on the GPU -> logits fp16 [M, vocab] ([1, vocab] for the last position only
-        when last_only, as a prefill needs)."""
+        when last_only, as a prefill needs). pick: see logits() (one-row steps)."""
         ext = ops.ext()
         m = tokens.shape[0]
         h = F.embedding(tokens, self.embed)
@@ -252,7 +259,7 @@ class FusedQwen2:
         if last_only:
             h, xn = h[-1:], xn[-1:]
         ext.rmsnorm(h, self.final_norm, self.eps, out=xn)
-        return self.logits(xn)
+        return self.logits(xn, pick if m == 1 else None)
 
     __call__ = forward
 
@@ -285,21 +292,29 @@ class FusedDecoder:
             raise ValueError("the cache has no room for a step after the prefill")
         self.positions.copy_(self.offsets + self.pos)
         # warm-up and capture on one stream, so the library's workspaces (keyed by stream) exist before capture
+        # one token per step: the head GEMV picks the greedy token for the next replay itself (into tokens, one
+        # position on; lowbit_f16_gemv_pick), else argmax and the feedback in torch. step() sets both buffers before
+        # each replay, so feeding given tokens is unaffected; greedy() runs replays back to back
+        pick = (self.tokens, self.positions) if self.chunk == 1 and self.f.head_picks() else None
         s = _native.capture_stream(self.tokens.device)
         s.wait_stream(torch.cuda.current_stream())
+        saved = (self.tokens.clone(), self.positions.clone())
         with torch.cuda.stream(s):
             for _ in range(warmup):
-                self.f(self.tokens, self.positions)
+                self.f(self.tokens, self.positions, pick=pick)
+                self.tokens.copy_(saved[0])
+                self.positions.copy_(saved[1])
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=s):
-            self.logits = self.f(self.tokens, self.positions)
-            self.next_token = self.logits[-1].argmax(-1)
-            if self.chunk == 1:
-                # greedy feedback for the next replay: the argmax becomes the input, one position on. step() sets both
-                # buffers before each replay, so feeding given tokens is unaffected; greedy() runs replays back to back
-                self.tokens.copy_(self.next_token.view(1))
-                self.positions.add_(1)
+            self.logits = self.f(self.tokens, self.positions, pick=pick)
+            if pick is not None:
+                self.next_token = self.tokens
+            else:
+                self.next_token = self.logits[-1].argmax(-1)
+                if self.chunk == 1:
+                    self.tokens.copy_(self.next_token.view(1))
+                    self.positions.add_(1)
         return self
 
     @torch.inference_mode()

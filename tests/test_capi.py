@@ -89,6 +89,18 @@ def _msg(rc):
 (lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, FAKE, 0, None), 3, "M must be positive"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, ctypes.c_void_p(4098), 4, None), 4, "4-byte aligned"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, None, 1 << 20, FAKE, None, None), 1, "null pointer"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, None, None, None), 1, "null pointer"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 60, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 65536, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 0, 64, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(ctypes.c_void_p(4104), FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, None), 4,
+     "16-byte aligned"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, ctypes.c_void_p(4100), 1 << 20, FAKE, None, None), 4,
+     "8-byte aligned"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, ctypes.c_void_p(4100), None), 4,
+     "8-byte aligned"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 151936, 64, FAKE, 1000, FAKE, None, None), 1, "workspace"),
     (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,
                                   None), 1, "at least 4096 bytes"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 5, 16, 128, None), 5, "1..4 rows"),

@@ -528,11 +528,11 @@ def test_capture_allocates_no_workspace(cuda, tiny_models, monkeypatch):
     created = []
     real = _native.workspace
 
-    def watching(device, stream, nbytes=_native.WORKSPACE_BYTES):
-        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes)
+    def watching(device, stream, nbytes=_native.WORKSPACE_BYTES, tag=""):
+        key = (device.index if device.index is not None else torch.cuda.current_device(), stream.value, nbytes, tag)
         if key not in _native._WORKSPACES:
             created.append((key, torch.cuda.is_current_stream_capturing()))
-        return real(device, stream, nbytes)
+        return real(device, stream, nbytes, tag)
 
     monkeypatch.setattr(_native, "workspace", watching)
     prompt = torch.randint(0, 1024, (1, 20), generator=torch.Generator(device="cuda").manual_seed(3), device="cuda")
