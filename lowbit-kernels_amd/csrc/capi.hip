@@ -585,7 +585,7 @@ int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* 
 
 int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
   if (!x || !w || !y) return fail(LOWBIT_ERR_ARG, "null pointer argument");
-  if (M < 1 || M > 4) return fail(LOWBIT_ERR_ROWS, "the fp16 GEMV takes 1..4 rows");
+  if (M < 1 || M > 16) return fail(LOWBIT_ERR_ROWS, "the fp16 GEMV takes 1..16 rows");
   if (N < 1 || K < 8 || K % 8 || !fits_int(N) || M * K * 2 > 65536 || (int64_t)8 * K * 2 > INT_MAX)
     return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 8 == 0 and M * K * 2 <= 65536");
   if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned");

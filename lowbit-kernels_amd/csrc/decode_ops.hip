@@ -440,17 +440,19 @@ __device__ __forceinline__ uint64_t pick_key(uint16_t b, int idx) {
 
 // PICK (M = 1): each workgroup also writes the key of its largest logit (as stored, fp16) to pick[blockIdx.x], for
 // head_pick_kernel
-template <int M, int RW, bool PICK = false>
+template <int M, int RW, int CH = kHeadChunks, bool PICK = false>
 __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                                       f16* __restrict__ y, int N, int K, uint64_t* __restrict__ pick) {
+                                                       f16* __restrict__ y, int N, int K, uint64_t* __restrict__ pick,
+                                                       int mrows) {
   static_assert(!PICK || M == 1, "the greedy pick takes one row");
+  // M rows compiled in, mrows <= M of them real (x staged and y stored for those; the rest computes on stale LDS)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
   // wave through readfirstlane: the row buffer resource below is then known uniform and stays in scalar registers
   // (from a per-lane value every weight load becomes a waterfall loop)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kp = K >> 3;                                     // 16-byte pieces per row
-  for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
+  for (int i = threadIdx.x; i < mrows * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
   __syncthreads();
   const int n0 = (blockIdx.x * 4 + wave) * RW;
   if (!PICK && n0 >= N) return;                             // (PICK: every wave reaches the barrier below; one past N
@@ -462,16 +464,16 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[r][m] = 0.f;
   const int nc = (kp + 63) >> 6;                             // 512-k chunks
-  for (int c0 = 0; c0 < nc; c0 += kHeadChunks) {
-    u32x4 wv[kHeadChunks][RW];
+  for (int c0 = 0; c0 < nc; c0 += CH) {
+    u32x4 wv[CH][RW];
 #pragma unroll
-    for (int u = 0; u < kHeadChunks; ++u) {
+    for (int u = 0; u < CH; ++u) {
       const int p = 64 * (c0 + u) + lane;                    // this lane's piece of the chunk
 #pragma unroll
       for (int r = 0; r < RW; ++r) wv[u][r] = buffer_load16_nt(wr, p < kp ? 2 * (r * K + 8 * p) : kOutOfRange);
     }
 #pragma unroll
-    for (int u = 0; u < kHeadChunks; ++u) {
+    for (int u = 0; u < CH; ++u) {
       const int p = 64 * (c0 + u) + lane;
       if (p >= kp) break;
 #pragma unroll
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       const float v = wave_sum(acc[r][m]);
-      if (lane == 0 && n0 + r < N) {
+      if (lane == 0 && n0 + r < N && m < mrows) {
         const f16 h = (f16)v;
         y[(size_t)m * N + n0 + r] = h;
         if constexpr (PICK) {
@@ -541,15 +543,88 @@ __global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t*
 
 constexpr int kHeadRows = 2;                                // RW: rows per wave (4 waves a workgroup)
 
-hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st) {
-  constexpr int RW = kHeadRows;
+// fp16-weight MFMA GEMV for the head at 9..16 rows, where the dot2 kernel above turns ALU-bound: each wave owns one
+// 16-row tile of W (the MFMA's A, straight from global: lane (r, q) takes row r, k = 128 c + 32 s + 8 q + 0..7 as
+// k-step s of chunk c, so one load instruction reads 64 contiguous bytes of each of 16 rows) against x staged whole in
+// LDS (B, the same k order; rows past M read row M - 1 and their columns are not stored), kF16wSlots chunks in
+// flight with the default cache policy, v_mfma_f32_16x16x32_f16 with fp32 accumulation. Lane l holds
+// y[l % 16][16 t + 4 (l / 16) + v], v = 0..3. On the 151936 x 2048 head at 16 rows (3 cold copies): 135 us against
+// 204 for hipBLASLt; 199 with non-temporal loads, whose half-used 128-byte lines were fetched twice; 141-151 with
+// 2-4 tiles a wave.
+constexpr int kF16wSlots = 4;
+__global__ __launch_bounds__(256) void gemm_f16w_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                                        f16* __restrict__ y, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4, kp = K >> 3, KC = K >> 7;
+  for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
+  __syncthreads();
+  const int t = blockIdx.x * 4 + wave, n0 = 16 * t;
+  if (n0 >= N) return;
+  const int rows = min(16, N - n0);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)n0 * K, (uint32_t)(rows * K * 2));
+  const int woff = r < rows ? 2 * (r * K + 8 * q) : kOutOfRange;
+  const int xrow = min(r, M - 1) * kp + q;                  // x piece (row, k / 8) in 16-byte units
+  u32x4 ring[kF16wSlots][4];
+  auto issue = [&](int d, int c) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) ring[d][s] = buffer_load16(wr, c < KC ? woff + 2 * (128 * c + 32 * s) : kOutOfRange);
+  };
+#pragma unroll
+  for (int d = 0; d < kF16wSlots; ++d) issue(d, d);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < KC; c0 += kF16wSlots) {
+#pragma unroll
+    for (int d = 0; d < kF16wSlots; ++d) {
+      const int c = c0 + d;
+      if (c < KC) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4 b = xs[xrow + 16 * c + 4 * s];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ring[d][s]),
+                                                       __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
+        }
+      }
+      issue(d, c + kF16wSlots);
+    }
+  }
+  const int n = n0 + 4 * q;
+  if (r < M && n < N) {
+    f16* dst = y + (size_t)r * N + n;
+    if (n + 4 <= N && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+      const f16x2 lo = {(f16)acc[0], (f16)acc[1]}, hi = {(f16)acc[2], (f16)acc[3]};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (n + v < N) dst[v] = (f16)acc[v];
+    }
+  }
+}
+
+namespace {
+template <int M, int RW, int CH>
+hipError_t launch_head(const f16* x, const f16* w, f16* y, int mrows, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + 4 * RW - 1) / (4 * RW))), block(256);
-  const size_t lds = (size_t)M * K * 2;
+  return launch(gemv_f16_kernel<M, RW, CH>, grid, block, (size_t)M * K * 2, st, x, w, y, N, K, nullptr, mrows);
+}
+}  // namespace
+
+hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st) {
   switch (M) {
-    case 1: return launch(gemv_f16_kernel<1, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
-    case 2: return launch(gemv_f16_kernel<2, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
-    case 3: return launch(gemv_f16_kernel<3, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
-    default: return launch(gemv_f16_kernel<4, RW>, grid, block, lds, st, x, w, y, N, K, nullptr);
+    case 1: return launch_head<1, kHeadRows, kHeadChunks>(x, w, y, 1, N, K, st);
+    case 2: return launch_head<2, kHeadRows, kHeadChunks>(x, w, y, 2, N, K, st);
+    case 3: return launch_head<3, kHeadRows, kHeadChunks>(x, w, y, 3, N, K, st);
+    case 4: return launch_head<4, kHeadRows, kHeadChunks>(x, w, y, 4, N, K, st);
+    // more rows: 8 weight rows per wave, two chunks in flight (the head, 3 cold copies: 8 rows 119.5 us against
+    // 126.6 for 4 per wave and 163.7 for 2; hipBLASLt 203.6. 16 rows: 206 us, level with hipBLASLt's 204: the dot2
+    // sequence per weight byte grows with the rows and the kernel turns ALU-bound)
+    default:
+      if (M <= 8) return launch_head<8, 8, 2>(x, w, y, M, N, K, st);
+      if (K % 128) return launch_head<16, 8, 2>(x, w, y, M, N, K, st);
+      return launch(gemm_f16w_kernel, dim3((unsigned)((N + 63) / 64)), dim3(256), (size_t)M * K * 2, st, x, w, y, M, N,
+                    K);
   }
 }
 
@@ -558,8 +633,8 @@ int head_pick_parts(int N) { return (N + 4 * kHeadRows - 1) / (4 * kHeadRows); }
 hipError_t head_pick_launch(const f16* x, const f16* w, f16* y, int N, int K, uint64_t* pick, int64_t* tokens,
                             int64_t* positions, hipStream_t st) {
   const int parts = head_pick_parts(N);
-  if (hipError_t e = launch(gemv_f16_kernel<1, kHeadRows, true>, dim3(parts), dim3(256), (size_t)K * 2, st, x, w, y, N,
-                            K, pick))
+  if (hipError_t e = launch(gemv_f16_kernel<1, kHeadRows, kHeadChunks, true>, dim3(parts), dim3(256), (size_t)K * 2, st,
+                            x, w, y, N, K, pick, 1))
     return e;
   return launch(head_pick_kernel, dim3(1), dim3(kPickThreads), 0, st, pick, parts, tokens, positions);
 }

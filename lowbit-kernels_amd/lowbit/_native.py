@@ -542,7 +542,7 @@ class NativeExt:
                                       aux, out)
 
     def f16_gemv(self, x, w, out=None):
-        """fp16 x [M <= 4, K] times fp16 W [N, K]^T -> fp16 [M, N] (fp32 accumulation)."""
+        """fp16 x [M <= 16, K] times fp16 W [N, K]^T -> fp16 [M, N] (fp32 accumulation)."""
         import torch
         if not (x.is_cuda and w.is_cuda and x.device == w.device):
             raise RuntimeError("x and w must be on the same GPU")

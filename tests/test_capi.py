@@ -103,7 +103,7 @@ def _msg(rc):
     (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 151936, 64, FAKE, 1000, FAKE, None, None), 1, "workspace"),
     (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,
                                   None), 1, "at least 4096 bytes"),
-    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 5, 16, 128, None), 5, "1..4 rows"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 17, 16, 128, None), 5, "1..16 rows"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 1, 16, 12, None), 3, "K % 8"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 4, 16, 16384, None), 3, "K % 8"),
     (lambda l: l.lowbit_f16_gemv(ctypes.c_void_p(4100), FAKE, FAKE, 1, 16, 128, None), 4, "16-byte"),
