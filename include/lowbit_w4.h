@@ -277,7 +277,8 @@ int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* 
                                 size_t workspace_bytes, void* stream);
 
 /* fp16 GEMV for the tied fp16 lm_head of a decode step (or the last row of a prefill): y [M, N] = fp16(x [M, K] . W^T)
- * with W fp16 [N, K] row-major, fp32 accumulation, 1 <= M <= 16, K % 8 == 0, M * K * 2 <= 65536, x and W 16-byte
+ * with W fp16 [N, K] row-major, fp32 accumulation, 1 <= M <= 64, K % 8 == 0 (K % 128 == 0 beyond 16 rows or where
+ * M * K * 2 > 65536), x and W 16-byte
  * aligned. No counterpart in the reference (its head is torch.nn.functional.linear, cuBLAS); it replaces that call
  * in the fused decoder, where hipBLASLt streams the 622 MB Qwen2.5-3B head at ~3 TB/s. */
 int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream);

@@ -585,9 +585,11 @@ int lowbit_f16_attention_linear(const void* q, const void* k_cache, const void* 
 
 int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
   if (!x || !w || !y) return fail(LOWBIT_ERR_ARG, "null pointer argument");
-  if (M < 1 || M > 16) return fail(LOWBIT_ERR_ROWS, "the fp16 GEMV takes 1..16 rows");
-  if (N < 1 || K < 8 || K % 8 || !fits_int(N) || M * K * 2 > 65536 || (int64_t)8 * K * 2 > INT_MAX)
-    return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 8 == 0 and M * K * 2 <= 65536");
+  if (M < 1 || M > 64) return fail(LOWBIT_ERR_ROWS, "the fp16 GEMV takes 1..64 rows");
+  if (N < 1 || K < 8 || K % 8 || !fits_int(N) || (int64_t)16 * K * 2 > INT_MAX || M * K * 2 > INT_MAX)
+    return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 8 == 0");
+  if ((M > 16 || M * K * 2 > 65536) && K % 128)
+    return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 128 == 0 beyond 16 rows or M * K * 2 > 65536");
   if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned");
   if (int rc = check_device()) return rc;
   return hip_status(gemv_f16_launch(static_cast<const f16*>(x), static_cast<const f16*>(w), static_cast<f16*>(y), (int)M,

@@ -543,63 +543,106 @@ __global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t*
 
 constexpr int kHeadRows = 2;                                // RW: rows per wave (4 waves a workgroup)
 
-// fp16-weight MFMA GEMV for the head at 9..16 rows, where the dot2 kernel above turns ALU-bound: each wave owns one
-// 16-row tile of W (the MFMA's A, straight from global: lane (r, q) takes row r, k = 128 c + 32 s + 8 q + 0..7 as
-// k-step s of chunk c, so one load instruction reads 64 contiguous bytes of each of 16 rows) against x staged whole in
-// LDS (B, the same k order; rows past M read row M - 1 and their columns are not stored), kF16wSlots chunks in
-// flight with the default cache policy, v_mfma_f32_16x16x32_f16 with fp32 accumulation. Lane l holds
-// y[l % 16][16 t + 4 (l / 16) + v], v = 0..3. On the 151936 x 2048 head at 16 rows (3 cold copies): 135 us against
-// 204 for hipBLASLt; 199 with non-temporal loads, whose half-used 128-byte lines were fetched twice; 141-151 with
-// 2-4 tiles a wave.
+// fp16-weight MFMA GEMV for the head beyond 8 rows (up to 64: MT 16-row activation tiles), where the dot2 kernel above
+// turns ALU-bound. Each wave owns one 16-row tile of W, the MFMA's A, straight from global: lane (r, q) takes row r,
+// k = 128 c + 32 s + 8 q + 0..7 as k-step s of chunk c, so one load instruction reads 64 contiguous bytes of each of
+// 16 rows (kF16wSlots chunks in flight, default cache policy: with non-temporal loads the half-used 128-byte lines
+// were fetched twice, 199 against 135 us). The workgroup's four waves share each 128-k chunk of x (B, the same k
+// order), staged by all 256 threads into one of two LDS buffers (16-byte pieces XOR-swizzled by row, so a B
+// fragment's 16 rows hit different banks) while the previous chunk is consumed, one barrier per chunk; rows past M
+// read zeros and are not stored. Lane l holds y[16 mt + l % 16][16 t + 4 (l / 16) + v], v = 0..3. On the 151936 x 2048
+// head (3 cold copies): 16 rows 135 us against 204 for hipBLASLt, 32 rows 142 against 146, 48 rows 152 against 144
+// (hipBLASLt keeps those), the same as with x staged whole in LDS at 16 rows.
 constexpr int kF16wSlots = 4;
-__global__ __launch_bounds__(256) void gemm_f16w_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
-                                                        f16* __restrict__ y, int M, int N, int K) {
+template <int MT>
+__global__ __launch_bounds__(256) void gemm_f16w_rows_kernel(const f16* __restrict__ x, const f16* __restrict__ w,
+                                                             f16* __restrict__ y, int M, int N, int K) {
+  constexpr int kRows = 16 * MT, kBuf = kRows * 256;        // one staged chunk of x: kRows rows x 256 bytes
+  constexpr int XP = kRows * 16 / 256;                     // 16-byte pieces a thread stages per chunk
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  u32x4* xs = reinterpret_cast<u32x4*>(smem);               // [M][K / 8]
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane & 15, q = lane >> 4, kp = K >> 3, KC = K >> 7;
-  for (int i = threadIdx.x; i < M * kp; i += blockDim.x) xs[i] = *reinterpret_cast<const u32x4*>(x + 8 * (size_t)i);
-  __syncthreads();
-  const int t = blockIdx.x * 4 + wave, n0 = 16 * t;
-  if (n0 >= N) return;
-  const int rows = min(16, N - n0);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)n0 * K, (uint32_t)(rows * K * 2));
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, q = lane >> 4, KC = K >> 7;
+  const int n0 = 16 * (blockIdx.x * 4 + wave);
+  const int rows = max(0, min(16, N - n0));
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(w + (size_t)min(n0, N) * K, (uint32_t)(rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, (uint32_t)(M * K * 2));
   const int woff = r < rows ? 2 * (r * K + 8 * q) : kOutOfRange;
-  const int xrow = min(r, M - 1) * kp + q;                  // x piece (row, k / 8) in 16-byte units
-  u32x4 ring[kF16wSlots][4];
+  auto slot = [](int row, int piece) { return 16 * (16 * row + (piece ^ (row & 15))); };   // byte offset in a buffer
+  int xoff[XP], xsl[XP];
+#pragma unroll
+  for (int u = 0; u < XP; ++u) {                            // piece p = tid + 256 u: row p / 16, piece p % 16
+    const int p = tid + 256 * u;
+    xoff[u] = (p >> 4) < M ? 2 * ((p >> 4) * K + 8 * (p & 15)) : kOutOfRange;
+    xsl[u] = slot(p >> 4, p & 15);
+  }
+  u32x4 ring[kF16wSlots][4], rx[XP];
   auto issue = [&](int d, int c) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) ring[d][s] = buffer_load16(wr, c < KC ? woff + 2 * (128 * c + 32 * s) : kOutOfRange);
   };
+  auto load_x = [&](int c) {
+#pragma unroll
+    for (int u = 0; u < XP; ++u) rx[u] = buffer_load16(xr, c < KC ? xoff[u] + 256 * c : kOutOfRange);
+  };
+  auto stage_x = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < XP; ++u) *reinterpret_cast<u32x4*>(smem + b * kBuf + xsl[u]) = rx[u];
+  };
+  load_x(0);
 #pragma unroll
   for (int d = 0; d < kF16wSlots; ++d) issue(d, d);
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  stage_x(0);
+  __syncthreads();
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int c0 = 0; c0 < KC; c0 += kF16wSlots) {
 #pragma unroll
     for (int d = 0; d < kF16wSlots; ++d) {
       const int c = c0 + d;
-      if (c < KC) {
+      if (c < KC) {                                         // uniform: every wave runs the same chunks
+        load_x(c + 1);
+        const uint8_t* xb = smem + (c & 1) * kBuf;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const u32x4 b = xs[xrow + 16 * c + 4 * s];
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ring[d][s]),
-                                                       __builtin_bit_cast(f16x8, b), acc, 0, 0, 0);
-        }
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const u32x4 b = *reinterpret_cast<const u32x4*>(xb + slot(16 * mt + r, 4 * s + q));
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, ring[d][s]),
+                                                             __builtin_bit_cast(f16x8, b), acc[mt], 0, 0, 0);
+          }
+        issue(d, c + kF16wSlots);
+        if (c + 1 < KC) stage_x((c + 1) & 1);
+        __syncthreads();
       }
-      issue(d, c + kF16wSlots);
     }
   }
-  const int n = n0 + 4 * q;
-  if (r < M && n < N) {
-    f16* dst = y + (size_t)r * N + n;
-    if (n + 4 <= N && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
-      const f16x2 lo = {(f16)acc[0], (f16)acc[1]}, hi = {(f16)acc[2], (f16)acc[3]};
-      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
-    } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        if (n + v < N) dst[v] = (f16)acc[v];
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r, n = n0 + 4 * q;
+    if (m < M && n < N) {
+      f16* dst = y + (size_t)m * N + n;
+      if (n + 4 <= N && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+        const f16x2 lo = {(f16)acc[mt][0], (f16)acc[mt][1]}, hi = {(f16)acc[mt][2], (f16)acc[mt][3]};
+        *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (n + v < N) dst[v] = (f16)acc[mt][v];
+      }
     }
+  }
+}
+
+hipError_t gemm_f16w_rows_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + 63) / 64)), block(256);
+  const int MT = (M + 15) / 16;
+  const size_t lds = (size_t)2 * 16 * MT * 256;
+  switch (MT) {
+    case 1: return launch(gemm_f16w_rows_kernel<1>, grid, block, lds, st, x, w, y, M, N, K);
+    case 2: return launch(gemm_f16w_rows_kernel<2>, grid, block, lds, st, x, w, y, M, N, K);
+    case 3: return launch(gemm_f16w_rows_kernel<3>, grid, block, lds, st, x, w, y, M, N, K);
+    default: return launch(gemm_f16w_rows_kernel<4>, grid, block, lds, st, x, w, y, M, N, K);
   }
 }
 
@@ -620,11 +663,12 @@ hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int
     // more rows: 8 weight rows per wave, two chunks in flight (the head, 3 cold copies: 8 rows 119.5 us against
     // 126.6 for 4 per wave and 163.7 for 2; hipBLASLt 203.6. 16 rows: 206 us, level with hipBLASLt's 204: the dot2
     // sequence per weight byte grows with the rows and the kernel turns ALU-bound)
-    default:
-      if (M <= 8) return launch_head<8, 8, 2>(x, w, y, M, N, K, st);
-      if (K % 128) return launch_head<16, 8, 2>(x, w, y, M, N, K, st);
-      return launch(gemm_f16w_kernel, dim3((unsigned)((N + 63) / 64)), dim3(256), (size_t)M * K * 2, st, x, w, y, M, N,
-                    K);
+    default: {
+      const bool x_fits = (size_t)M * K * 2 <= 65536;      // the dot2 kernels stage x whole
+      if (M <= 8 && x_fits) return launch_head<8, 8, 2>(x, w, y, M, N, K, st);
+      if (K % 128) return x_fits && M <= 16 ? launch_head<16, 8, 2>(x, w, y, M, N, K, st) : hipErrorInvalidValue;
+      return gemm_f16w_rows_launch(x, w, y, M, N, K, st);
+    }
   }
 }
 

@@ -188,13 +188,14 @@ class FusedQwen2:
         return self.hidden * 2 <= 65536
 
     def logits(self, xn, pick=None):
-        """The tied fp16 head: the library's fp16 GEMV for up to 16 rows (hipBLASLt streams the head at ~3 TB/s at
-        these shapes: 94 against 202 us at one row, 120 against 204 at 8, 135 against 204 at 16), hipBLASLt beyond.
-        pick = (tokens, positions), one row (head_picks()): the GEMV also writes the greedy pick to tokens[0] and
-        advances positions[0]."""
+        """The tied fp16 head: the library's fp16 GEMV for up to 32 rows (hipBLASLt streams the head at ~3 TB/s at
+        these shapes: 94 against 202 us at one row, 120 against 204 at 8, 135 against 204 at 16, 142 against 146 at
+        32), hipBLASLt beyond (144 against 152 at 48). pick = (tokens, positions), one row (head_picks()): the GEMV
+        also writes the greedy pick to tokens[0] and advances positions[0]."""
         if pick is not None:
             return ops.ext().f16_gemv_pick(xn, self.head, pick[0], pick[1])
-        if xn.shape[0] <= 16 and xn.shape[1] * xn.shape[0] * 2 <= 65536:
+        m, k = xn.shape
+        if (m <= 8 and m * k * 2 <= 65536) or (m <= 32 and k % 128 == 0):
             return ops.ext().f16_gemv(xn, self.head)
         return F.linear(xn, self.head)
 

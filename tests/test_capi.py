@@ -84,9 +84,9 @@ def _msg(rc):
                                          FAKE, FAKE, 2, 1, 64, None, ctypes.c_float(0), None, 0, None), 4, "16-byte aligned rope table"),
     (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 4, 512, 128, 128, FAKE, FAKE, FAKE, FAKE,
                                          ctypes.c_void_p(4098), FAKE, 2, 1, 64, None, ctypes.c_float(0), None, 0, None), 4, "8-byte aligned"),
-        (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 100, 512, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
+    (lambda l: l.lowbit_w4_qkv_rope_rows(FAKE, FAKE, FAKE, 100, 512, 128, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 1,
                                          64, FAKE, ctypes.c_float(1e-6), None, 0, None), 1, "at most 64 rows"),
-(lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
+    (lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, FAKE, 0, None), 3, "M must be positive"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, ctypes.c_void_p(4098), 4, None), 4, "4-byte aligned"),
     (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, None, 1 << 20, FAKE, None, None), 1, "null pointer"),
@@ -103,9 +103,10 @@ def _msg(rc):
     (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 151936, 64, FAKE, 1000, FAKE, None, None), 1, "workspace"),
     (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,
                                   None), 1, "at least 4096 bytes"),
-    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 17, 16, 128, None), 5, "1..16 rows"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 65, 16, 128, None), 5, "1..64 rows"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 17, 16, 136, None), 3, "K % 128"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 1, 16, 12, None), 3, "K % 8"),
-    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 4, 16, 16384, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 4, 16, 16392, None), 3, "K % 128"),
     (lambda l: l.lowbit_f16_gemv(ctypes.c_void_p(4100), FAKE, FAKE, 1, 16, 128, None), 4, "16-byte"),
     (lambda l: l.lowbit_hbm_read(None, 1024, FAKE, 256, None), 1, "null pointer"),
     (lambda l: l.lowbit_hbm_read(FAKE, 1000, FAKE, 256, None), 3, "multiple of 16"),

@@ -108,14 +108,16 @@ def test_fused_input_norm_on_the_mfma_gemm(cuda, k, n):
 @pytest.mark.parametrize("n,k", [(1000, 2048), (4099, 1536), (64, 8), (151936, 2048), (7, 16384), (1001, 384),
                                  (33, 1000)])
 def test_f16_gemv_against_fp32(cuda, n, k):
-    """The fp16 head GEMV, 1 to 16 rows: the fp16 rounding of the exact product, up to fp32 summation noise (half an
+    """The fp16 head GEMV, 1 to 64 rows: the fp16 rounding of the exact product, up to fp32 summation noise (half an
     fp16 ulp plus 2^-16 of the output RMS); up to 8 rows (the dot2 kernel) each row the same bits as that row alone (a
-    row's sum does not depend on how many rows share the call), 9..16 rows (the MFMA kernel where K % 128 == 0) the
-    same bits on every call."""
+    row's sum does not depend on how many rows share the call), beyond (the MFMA kernel where K % 128 == 0) the same
+    bits on every call; more rows than the dot2 kernel holds are refused where K % 128 != 0."""
     g = torch.Generator(device="cuda").manual_seed(n + k)
     w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
-    for m in (1, 2, 3, 4, 5, 8, 9, 16):
-        if m * k * 2 > 65536:
+    for m in (1, 2, 3, 4, 5, 8, 9, 16, 17, 33, 64):
+        if (m > 16 or m * k * 2 > 65536) and k % 128:
+            with pytest.raises(RuntimeError, match="K % 128"):
+                ops.ext().f16_gemv(torch.zeros(m, k, dtype=torch.half, device="cuda"), w)
             continue
         x = torch.randn(m, k, generator=g, device="cuda").half()
         y = ops.ext().f16_gemv(x, w)
@@ -127,8 +129,9 @@ def test_f16_gemv_against_fp32(cuda, n, k):
             for r in (0, m // 2, m - 1):
                 assert torch.equal(y[r:r + 1], ops.ext().f16_gemv(x[r:r + 1].contiguous(), w)), (n, k, m, r)
         assert torch.equal(y, ops.ext().f16_gemv(x, w)), (n, k, m)
-    with pytest.raises(RuntimeError, match="1..16 rows"):
-        ops.ext().f16_gemv(torch.zeros(17, 8, dtype=torch.half, device="cuda"), w[:, :8].contiguous())
+    with pytest.raises(RuntimeError, match="1..64 rows"):
+        ops.ext().f16_gemv(torch.zeros(65, 128, dtype=torch.half, device="cuda"), torch.zeros(8, 128, dtype=torch.half,
+                                                                                               device="cuda"))
 
 
 def test_rmsnorm_matches_qwen2_rmsnorm(cuda):
