@@ -631,7 +631,10 @@ def progress(msg):
 
 def traced_gemv(a):
     """The timed workload (this script with --trace-child: pool, warm-up, capture, one untimed and `replays` timed
-    replays of the K-step graph) run under `rocprofv3 --kernel-trace`, before this process touches the GPU. Returns
+    replays of the K-step graph) run under `rocprofv3 --kernel-trace --stats`, the command whose summary is kept with
+    the profiles (with the same --steps, --warmup and --replays: the same trace taken standalone on one box averaged
+    3.89 us per GEMV dispatch against 3.80 here, while 20-step graphs average 4.62), before this process touches the
+    GPU. Returns
     the durations of the GEMV dispatches of the timed replays (the last replays x steps x 14 of them) from the trace's
     own start / end stamps, the traced replays' wall time per launch (first start to last end: the tracer's gaps
     between dispatches), and per-instance averages; None when rocprofv3 is missing or the run fails."""
@@ -644,7 +647,7 @@ def traced_gemv(a):
     if prof is None:
         return None
     tmp = tempfile.mkdtemp(prefix="lowbit_trace_")
-    cmd = [prof, "--kernel-trace", "--output-format", "csv", "-d", tmp, "-o", "head", "--", sys.executable, "-u",
+    cmd = [prof, "--kernel-trace", "--stats", "--output-format", "csv", "-d", tmp, "-o", "head", "--", sys.executable, "-u",
            str(ROOT / "bench.py"), "--trace-child", "--steps", str(a.steps), "--warmup", str(a.warmup), "--replays",
            str(a.replays)]
     try:
