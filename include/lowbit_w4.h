@@ -286,11 +286,15 @@ int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N,
 /* lowbit_f16_gemv for one row followed by the greedy pick and its feedback (replaces the reference harness's
  * lg.argmax(-1) and the copy that feeds the pick back as the next step's input, bench/e2e.py:93-95): y [1, N] as
  * lowbit_f16_gemv writes it, then tokens[0] = the index of the largest of y as torch.argmax picks it (the first of
- * equal maxima, -0 equal to +0, a NaN above every number) and positions[0] += 1 (positions may be NULL). Two launches,
- * no allocation and no memset, so a decode step may capture it; workspace (8-byte aligned) holds a 64-bit key per
- * head workgroup, 8 * ceil(N / 8) bytes, and needs no initial contents. */
+ * equal maxima, -0 equal to +0, a NaN above every number) and positions[0] += 1 (positions may be NULL); with
+ * out_tokens and out_count (both or neither), out_tokens[*out_count] = the pick while *out_count < out_capacity, then
+ * *out_count += 1; with embed (the tied embedding [N, K], 16-byte aligned) and h_out (both or neither), h_out [K] =
+ * the pick's embedding row, the next step's input (replaces the reference harness's embedding lookup of the fed-back
+ * token). Two launches, no allocation and no memset, so a decode step may capture it; workspace (8-byte aligned) holds
+ * a 64-bit key per head workgroup, 8 * ceil(N / 8) bytes, and needs no initial contents. */
 int lowbit_f16_gemv_pick(const void* x, const void* w, void* y, int64_t N, int64_t K, void* workspace,
-                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, void* stream);
+                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, int64_t* out_tokens,
+                         int64_t out_capacity, int32_t* out_count, const void* embed, void* h_out, void* stream);
 
 /* ---- HBM bandwidth probes (the measured peak that kernel bandwidths are quoted against) ----
  * The reference measures its peak with a torch device copy and a torch sum over 256 MiB (bench/gpu_run.py:133-141);

@@ -598,8 +598,17 @@ int lowbit_f16_gemv(const void* x, const void* w, void* y, int64_t M, int64_t N,
 }
 
 int lowbit_f16_gemv_pick(const void* x, const void* w, void* y, int64_t N, int64_t K, void* workspace,
-                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, void* stream) {
+                         size_t workspace_bytes, int64_t* tokens, int64_t* positions, int64_t* out_tokens,
+                         int64_t out_capacity, int32_t* out_count, const void* embed, void* h_out, void* stream) {
   if (!x || !w || !y || !workspace || !tokens) return fail(LOWBIT_ERR_ARG, "null pointer argument");
+  if (!out_tokens != !out_count || !embed != !h_out)
+    return fail(LOWBIT_ERR_ARG, "out_tokens goes with out_count, embed with h_out");
+  if (out_count && (out_capacity < 0 || !fits_int(out_capacity)))
+    return fail(LOWBIT_ERR_SHAPE, "f16_gemv_pick: out_capacity must be a non-negative 32-bit count");
+  if (embed && (!aligned16(embed) || !aligned16(h_out)))
+    return fail(LOWBIT_ERR_ALIGN, "f16_gemv_pick: embed and h_out must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(out_tokens) & 7) || (reinterpret_cast<uintptr_t>(out_count) & 3))
+    return fail(LOWBIT_ERR_ALIGN, "f16_gemv_pick needs naturally aligned out_tokens and out_count");
   if (N < 1 || K < 8 || K % 8 || !fits_int(N) || K * 2 > 65536)
     return fail(LOWBIT_ERR_SHAPE, "the fp16 GEMV takes K % 8 == 0 and K * 2 <= 65536");
   if (!aligned16(x) || !aligned16(w)) return fail(LOWBIT_ERR_ALIGN, "x and w must be 16-byte aligned");
@@ -612,8 +621,9 @@ int lowbit_f16_gemv_pick(const void* x, const void* w, void* y, int64_t N, int64
                 (long long)N);
   if (int rc = check_device()) return rc;
   return hip_status(head_pick_launch(static_cast<const f16*>(x), static_cast<const f16*>(w), static_cast<f16*>(y),
-                                     (int)N, (int)K, static_cast<uint64_t*>(workspace), tokens, positions,
-                                     static_cast<hipStream_t>(stream)),
+                                     (int)N, (int)K, static_cast<uint64_t*>(workspace), tokens, positions, out_tokens,
+                                     (int)out_capacity, out_count, static_cast<const f16*>(embed),
+                                     static_cast<f16*>(h_out), static_cast<hipStream_t>(stream)),
                     "f16_gemv_pick");
 }
 

@@ -514,11 +514,16 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(const f16* __restrict__ x
 }
 
 // The greedy pick and its feedback, one workgroup: the largest of the head workgroups' keys (pick[0 .. n)) gives the
-// index; tokens[0] = index, positions[0] += 1 (positions may be null)
+// index; tokens[0] = index, positions[0] += 1 (positions may be null), out[*out_count] = index while *out_count <
+// out_cap and *out_count + 1 (out_count may be null), and h_out[0 .. H) = embed row index (embed may be null): the next
+// step's input, so that a one-token step needs no embedding gather of its own
 constexpr int kPickThreads = 1024;
 __global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t* __restrict__ pick, int n,
-                                                                 int64_t* tokens, int64_t* positions) {
+                                                                 int64_t* tokens, int64_t* positions, int64_t* out,
+                                                                 int out_cap, int* out_count,
+                                                                 const f16* __restrict__ embed, int H, f16* h_out) {
   __shared__ uint64_t red[kPickThreads / 64];
+  __shared__ int s_idx;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   uint64_t best = 0;
   for (int i0 = tid; i0 < n; i0 += 8 * kPickThreads) {      // eight loads in flight per thread
@@ -535,10 +540,22 @@ __global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t*
   }
   if (lane == 0) red[wave] = best;
   __syncthreads();
-  if (tid != 0) return;
-  for (int v = 1; v < kPickThreads / 64; ++v) best = red[v] > best ? red[v] : best;
-  tokens[0] = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
-  if (positions) positions[0] += 1;
+  if (tid == 0) {
+    for (int v = 1; v < kPickThreads / 64; ++v) best = red[v] > best ? red[v] : best;
+    const int idx = (int)(0xFFFFFFFFu - (uint32_t)best);
+    s_idx = idx;
+    tokens[0] = idx;
+    if (positions) positions[0] += 1;
+    if (out_count) {
+      const int c = *out_count;
+      if (c < out_cap) out[c] = idx;
+      *out_count = c + 1;
+    }
+  }
+  if (embed == nullptr) return;                              // (uniform)
+  __syncthreads();
+  const u32x4* src = reinterpret_cast<const u32x4*>(embed + (size_t)s_idx * H);
+  for (int i = tid; i < (H >> 3); i += kPickThreads) reinterpret_cast<u32x4*>(h_out)[i] = src[i];
 }
 
 constexpr int kHeadRows = 2;                                // RW: rows per wave (4 waves a workgroup)
@@ -675,12 +692,14 @@ hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int
 int head_pick_parts(int N) { return (N + 4 * kHeadRows - 1) / (4 * kHeadRows); }
 
 hipError_t head_pick_launch(const f16* x, const f16* w, f16* y, int N, int K, uint64_t* pick, int64_t* tokens,
-                            int64_t* positions, hipStream_t st) {
+                            int64_t* positions, int64_t* out, int out_cap, int* out_count, const f16* embed, f16* h_out,
+                            hipStream_t st) {
   const int parts = head_pick_parts(N);
   if (hipError_t e = launch(gemv_f16_kernel<1, kHeadRows, kHeadChunks, true>, dim3(parts), dim3(256), (size_t)K * 2, st,
                             x, w, y, N, K, pick, 1))
     return e;
-  return launch(head_pick_kernel, dim3(1), dim3(kPickThreads), 0, st, pick, parts, tokens, positions);
+  return launch(head_pick_kernel, dim3(1), dim3(kPickThreads), 0, st, pick, parts, tokens, positions, out, out_cap,
+                out_count, embed, K, h_out);
 }
 
 hipError_t rmsnorm_launch(const f16* x, const f16* w, f16* out, int M, int H, float eps, hipStream_t st) {

@@ -310,7 +310,8 @@ hipError_t rope_kv_launch(const f16* qkv, const int64_t* pos, const float* inv_f
 hipError_t gemv_f16_launch(const f16* x, const f16* w, f16* y, int M, int N, int K, hipStream_t st);
 int head_pick_parts(int N);                                  // 64-bit keys head_pick_launch keeps in its workspace
 hipError_t head_pick_launch(const f16* x, const f16* w, f16* y, int N, int K, uint64_t* pick, int64_t* tokens,
-                            int64_t* positions, hipStream_t st);
+                            int64_t* positions, int64_t* out, int out_cap, int* out_count, const f16* embed, f16* h_out,
+                            hipStream_t st);
 hipError_t hbm_read_launch(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t stream);
 hipError_t hbm_copy_launch(const void* src, void* dst, size_t bytes, int blocks, hipStream_t stream);
 hipError_t attention_launch(const f16* q, const f16* k, const f16* v, const int64_t* pos, f16* out, int M, int Hq,

@@ -52,7 +52,8 @@ SIGNATURES = {
     "lowbit_attention": ([_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, ctypes.c_size_t,
                           _vp], _int),
     "lowbit_f16_gemv": ([_vp, _vp, _vp, _i64, _i64, _i64, _vp], _int),
-    "lowbit_f16_gemv_pick": ([_vp, _vp, _vp, _i64, _i64, _vp, ctypes.c_size_t, _vp, _vp, _vp], _int),
+    "lowbit_f16_gemv_pick": ([_vp, _vp, _vp, _i64, _i64, _vp, ctypes.c_size_t, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp],
+                             _int),
     "lowbit_w4_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _vp, _i64,
                                     _i64, _int, _vp, _vp, ctypes.c_size_t, _vp], _int),
     "lowbit_f16_attention_linear": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_float, _vp, _vp, _i64, _int,
@@ -557,9 +558,12 @@ class NativeExt:
                                            _stream(x.device)))
         return y
 
-    def f16_gemv_pick(self, x, w, tokens, positions=None, out=None):
+    def f16_gemv_pick(self, x, w, tokens, positions=None, out=None, out_tokens=None, out_count=None, embed=None,
+                      h_out=None):
         """f16_gemv for one row, then the greedy pick on the GPU: tokens[0] = argmax of the logits (torch.argmax's
-        choice among equal maxima and NaNs), positions[0] += 1 (int64, or None); returns the logits [1, N]."""
+        choice among equal maxima and NaNs), positions[0] += 1 (int64, or None); returns the logits [1, N].
+        out_tokens (int64) with out_count (int32 [1]): out_tokens[out_count] = the pick while out_count <
+        out_tokens.numel(), then out_count += 1. embed ([N, K] fp16) with h_out ([1, K] fp16): h_out = embed[pick]."""
         import torch
         if x.dim() != 2 or x.shape[0] != 1:
             raise RuntimeError("f16_gemv_pick takes one row x [1, K]")
@@ -572,14 +576,26 @@ class NativeExt:
         for name, t in (("tokens", tokens), ("positions", positions)):   # element 0 is written
             if t is not None and (t.dtype != torch.int64 or not t.is_contiguous() or t.device != x.device or t.numel() < 1):
                 raise RuntimeError(f"{name} must be a contiguous int64 tensor of at least one element on {x.device}")
+        if (out_tokens is None) != (out_count is None) or (embed is None) != (h_out is None):
+            raise RuntimeError("out_tokens goes with out_count, embed with h_out")
+        if out_tokens is not None:
+            if out_tokens.dtype != torch.int64 or not out_tokens.is_contiguous() or out_tokens.device != x.device:
+                raise RuntimeError(f"out_tokens must be a contiguous int64 tensor on {x.device}")
+            _need(out_count, "out_count", torch.int32, (1,), x.device)
+        if embed is not None:
+            _need(embed, "embed", torch.float16, tuple(w.shape), x.device)
+            _need(h_out, "h_out", torch.float16, (1, x.shape[1]), x.device)
         n = w.shape[0]
         y = out if out is not None else torch.empty((1, n), dtype=torch.float16, device=x.device)
         _need(y, "out", torch.float16, (1, n), x.device)
         with _DeviceGuard(x.device):
             st = _stream(x.device)
             ws = workspace(x.device, st, max(PICK_WORKSPACE_BYTES, 8 * (-(-n // 8))), tag="pick")
+            opt = lambda t: ptr(t) if t is not None else None
             check(self.lib.lowbit_f16_gemv_pick(ptr(x), ptr(w), ptr(y), n, x.shape[1], ptr(ws), ws.numel(), ptr(tokens),
-                                                ptr(positions) if positions is not None else None, st))
+                                                opt(positions), opt(out_tokens),
+                                                out_tokens.numel() if out_tokens is not None else 0, opt(out_count),
+                                                opt(embed), opt(h_out), st))
         return y
 
     def _check_f16_weight(self, x, w):

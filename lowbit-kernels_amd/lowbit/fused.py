@@ -190,22 +190,27 @@ class FusedQwen2:
     def logits(self, xn, pick=None):
         """The tied fp16 head: the library's fp16 GEMV for up to 32 rows (hipBLASLt streams the head at ~3 TB/s at
         these shapes: 94 against 202 us at one row, 120 against 204 at 8, 135 against 204 at 16, 142 against 146 at
-        32), hipBLASLt beyond (144 against 152 at 48). pick = (tokens, positions), one row (head_picks()): the GEMV
-        also writes the greedy pick to tokens[0] and advances positions[0]."""
+        32), hipBLASLt beyond (144 against 152 at 48). pick = (tokens, positions[, out_tokens, out_count, h_next]),
+        one row (head_picks()): the GEMV also writes the greedy pick to tokens[0], advances positions[0] and, given
+        the rest, appends the pick to out_tokens and writes its embedding row to h_next (the next step's input)."""
         if pick is not None:
-            return ops.ext().f16_gemv_pick(xn, self.head, pick[0], pick[1])
+            more = {}
+            if len(pick) > 2:
+                more = dict(out_tokens=pick[2], out_count=pick[3], embed=self.embed, h_out=pick[4])
+            return ops.ext().f16_gemv_pick(xn, self.head, pick[0], pick[1], **more)
         m, k = xn.shape
         if (m <= 8 and m * k * 2 <= 65536) or (m <= 32 and k % 128 == 0):
             return ops.ext().f16_gemv(xn, self.head)
         return F.linear(xn, self.head)
 
     @torch.inference_mode()
-    def forward(self, tokens, positions, last_only=False, pick=None):
+    def forward(self, tokens, positions, last_only=False, pick=None, h=None):
         """tokens, positions: int64 [M] on the GPU -> logits fp16 [M, vocab] ([1, vocab] for the last position only
-        when last_only, as a prefill needs). pick: see logits() (one-row steps)."""
+        when last_only, as a prefill needs). pick: see logits() (one-row steps). h: the tokens' embedding rows
+        [M, hidden] when the caller already holds them (it becomes the residual stream, overwritten)."""
         ext = ops.ext()
         m = tokens.shape[0]
-        h = F.embedding(tokens, self.embed)
+        h = F.embedding(tokens, self.embed) if h is None else h
         xn = torch.empty_like(h)
         q = torch.empty(m, self.hq, self.head_dim, dtype=torch.float16, device=h.device)
         attn = torch.empty(m, self.hq * self.head_dim, dtype=torch.float16, device=h.device)
@@ -275,6 +280,7 @@ class FusedDecoder:
         self.tokens = torch.zeros(chunk, dtype=torch.long, device=dev)
         self.positions = torch.zeros(chunk, dtype=torch.long, device=dev)
         self.offsets = torch.arange(chunk, dtype=torch.long, device=dev)
+        self.h = None                                       # the step's embedding rows when the head picks (capture)
         self.pos = 0
         self.graph = self.logits = self.next_token = None
 
@@ -295,21 +301,30 @@ class FusedDecoder:
         self.positions.copy_(self.offsets + self.pos)
         # warm-up and capture on one stream, so the library's workspaces (keyed by stream) exist before capture
         # one token per step: the head GEMV picks the greedy token for the next replay itself (into tokens, one
-        # position on; lowbit_f16_gemv_pick), else argmax and the feedback in torch. step() sets both buffers before
-        # each replay, so feeding given tokens is unaffected; greedy() runs replays back to back
-        pick = (self.tokens, self.positions) if self.chunk == 1 and self.f.head_picks() else None
+        # position on, appended to out_tokens, its embedding row into h; lowbit_f16_gemv_pick), else argmax and the
+        # feedback in torch. step() sets the buffers before each replay, so feeding given tokens is unaffected;
+        # greedy() runs replays back to back
+        pick, h = None, None
+        if self.chunk == 1 and self.f.head_picks():
+            dev = self.tokens.device
+            self.h = F.embedding(self.tokens, self.f.embed)
+            self.out_tokens = torch.zeros(self.f.max_len, dtype=torch.long, device=dev)
+            self.out_count = torch.zeros(1, dtype=torch.int32, device=dev)
+            pick, h = (self.tokens, self.positions, self.out_tokens, self.out_count, self.h), self.h
         s = _native.capture_stream(self.tokens.device)
         s.wait_stream(torch.cuda.current_stream())
-        saved = (self.tokens.clone(), self.positions.clone())
+        saved = (self.tokens.clone(), self.positions.clone(), None if h is None else h.clone())
         with torch.cuda.stream(s):
             for _ in range(warmup):
-                self.f(self.tokens, self.positions, pick=pick)
+                self.f(self.tokens, self.positions, pick=pick, h=h)
                 self.tokens.copy_(saved[0])
                 self.positions.copy_(saved[1])
+                if h is not None:
+                    h.copy_(saved[2])
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph, stream=s):
-            self.logits = self.f(self.tokens, self.positions, pick=pick)
+            self.logits = self.f(self.tokens, self.positions, pick=pick, h=h)
             if pick is not None:
                 self.next_token = self.tokens
             else:
@@ -332,11 +347,14 @@ class FusedDecoder:
             self.pos += 1
         return out
 
+    @torch.inference_mode()
     def step(self, tokens):
         if self.pos + self.chunk > self.f.max_len:
             raise ValueError("the cache is full")
         self.tokens.copy_(tokens.view(self.chunk))
         self.positions.copy_(self.offsets + self.pos)
+        if self.h is not None:
+            torch.index_select(self.f.embed, 0, self.tokens, out=self.h)
         self.graph.replay()
         self.pos += self.chunk
         return self.logits
@@ -351,6 +369,14 @@ class FusedDecoder:
         out[0] = first
         self.tokens.copy_(out[:1])
         self.positions.fill_(self.pos)
+        if self.h is not None:                              # the graph appends its picks and gathers their rows
+            torch.index_select(self.f.embed, 0, self.tokens, out=self.h)
+            self.out_count.zero_()
+            for _ in range(1, n):
+                self.graph.replay()
+            self.pos += n - 1
+            out[1:] = self.out_tokens[:n - 1]
+            return out
         for i in range(1, n):                               # the graph feeds its argmax back (capture)
             self.graph.replay()
             self.pos += 1

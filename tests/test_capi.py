@@ -89,18 +89,37 @@ def _msg(rc):
     (lambda l: l.lowbit_rope_table(FAKE, None, FAKE, 4, None), 1, "null pointer"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, FAKE, 0, None), 3, "M must be positive"),
     (lambda l: l.lowbit_rope_table(FAKE, FAKE, ctypes.c_void_p(4098), 4, None), 4, "4-byte aligned"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, None, 1 << 20, FAKE, None, None), 1, "null pointer"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, None, None, None), 1, "null pointer"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 60, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 65536, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 0, 64, FAKE, 1 << 20, FAKE, None, None), 3, "K % 8"),
-    (lambda l: l.lowbit_f16_gemv_pick(ctypes.c_void_p(4104), FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, None), 4,
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, None, 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 1, "null pointer"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20,
+                                      None, None, None, 0, None, None, None, None), 1, "null pointer"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 60, FAKE, 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 65536, FAKE, 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 0, 64, FAKE, 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 3, "K % 8"),
+    (lambda l: l.lowbit_f16_gemv_pick(ctypes.c_void_p(4104), FAKE, FAKE, 100, 64, FAKE, 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 4,
      "16-byte aligned"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, ctypes.c_void_p(4100), 1 << 20, FAKE, None, None), 4,
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, ctypes.c_void_p(4100), 1 << 20,
+                                      FAKE, None, None, 0, None, None, None, None), 4,
      "8-byte aligned"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, ctypes.c_void_p(4100), None), 4,
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20,
+                                      FAKE, ctypes.c_void_p(4100), None, 0, None, None, None, None), 4,
      "8-byte aligned"),
-    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 151936, 64, FAKE, 1000, FAKE, None, None), 1, "workspace"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 151936, 64, FAKE, 1000,
+                                      FAKE, None, None, 0, None, None, None, None), 1, "workspace"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, FAKE, 4, None, None, None,
+                                      None), 1, "out_tokens goes with out_count"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, None, 0, None, FAKE, None,
+                                      None), 1, "embed with h_out"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, FAKE, -1, FAKE, None, None,
+                                      None), 3, "out_capacity"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, None, 0, None,
+                                      ctypes.c_void_p(4104), FAKE, None), 4, "embed and h_out must be 16-byte"),
+    (lambda l: l.lowbit_f16_gemv_pick(FAKE, FAKE, FAKE, 100, 64, FAKE, 1 << 20, FAKE, None, FAKE, 4,
+                                      ctypes.c_void_p(4098), None, None, None), 4, "naturally aligned"),
     (lambda l: l.lowbit_attention(FAKE, FAKE, FAKE, FAKE, FAKE, 1, 2, 1, 64, 64, ctypes.c_float(1.0), FAKE, 1024,
                                   None), 1, "at least 4096 bytes"),
     (lambda l: l.lowbit_f16_gemv(FAKE, FAKE, FAKE, 65, 16, 128, None), 5, "1..64 rows"),

@@ -84,3 +84,29 @@ def test_feedback_and_graph_replays(cuda):
         want = ops.ext().f16_gemv(x, w)
         assert torch.equal(y, want) and int(tokens.item()) == int(torch.argmax(want[0]).item())
         assert int(positions.item()) == i + 1
+
+
+def test_append_and_next_embedding(cuda):
+    """out_tokens / out_count: each call appends its pick while there is room and counts on past it; embed / h_out:
+    h_out is the pick's row of embed, which may be a tensor other than the head (an untied embedding)."""
+    gen = torch.Generator().manual_seed(6)
+    n, k = 4099, 1536
+    w = (torch.randn(n, k, generator=gen) * 0.05).half().cuda()
+    embed = torch.randn(n, k, generator=gen).half().cuda()
+    tokens = torch.zeros(1, dtype=torch.long, device="cuda")
+    out_tokens = torch.full((3,), -1, dtype=torch.long, device="cuda")
+    out_count = torch.zeros(1, dtype=torch.int32, device="cuda")
+    h = torch.zeros(1, k, dtype=torch.half, device="cuda")
+    picks = []
+    for i in range(5):
+        x = torch.randn(1, k, generator=gen).half().cuda()
+        y = ops.ext().f16_gemv_pick(x, w, tokens, None, out_tokens=out_tokens, out_count=out_count, embed=embed, h_out=h)
+        tok = int(torch.argmax(y[0]).item())
+        picks.append(tok)
+        assert int(tokens.item()) == tok and int(out_count.item()) == i + 1
+        assert torch.equal(h[0], embed[tok]), i
+    assert out_tokens.tolist() == picks[:3]
+    with pytest.raises(RuntimeError, match="goes with"):
+        ops.ext().f16_gemv_pick(x, w, tokens, out_tokens=out_tokens)
+    with pytest.raises(RuntimeError, match="h_out"):
+        ops.ext().f16_gemv_pick(x, w, tokens, embed=embed, h_out=h[:, :8])
