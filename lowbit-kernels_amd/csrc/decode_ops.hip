@@ -547,9 +547,9 @@ __global__ __launch_bounds__(kPickThreads) void head_pick_kernel(const uint64_t*
     tokens[0] = idx;
     if (positions) positions[0] += 1;
     if (out_count) {
-      const int c = *out_count;
-      if (c < out_cap) out[c] = idx;
-      *out_count = c + 1;
+      const unsigned c = (unsigned)*out_count;               // (a count past INT_MAX stays out of range)
+      if (c < (unsigned)out_cap) out[c] = idx;
+      *out_count = (int)(c + 1u);
     }
   }
   if (embed == nullptr) return;                              // (uniform)
