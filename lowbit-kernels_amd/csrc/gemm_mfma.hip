@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
   constexpr bool kWhole = kPieces % kGroupThreads == 0;    // else the last round of pieces is partial
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_last;
-  args_in_sgprs(x, w, s, y, M, N, K, G, S, ctr, part, epi.aux);
+  args_in_sgprs(x, w, s, y, M, N, K, G, S, ctr, part, epi.aux, (int)gridDim.y);   // (the grid's line: the order)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = wave / TW, tw = wave - kg * TW;            // K-group, tile-wave
