@@ -261,6 +261,14 @@ __device__ __forceinline__ f16 epi_value(int mode, const f16* __restrict__ aux, 
   return v;
 }
 
+// epi_value with its bias or residual element a already loaded (the same arithmetic)
+__device__ __forceinline__ f16 epi_apply(int mode, f16 a, float acc) {
+  const f16 v = (f16)acc;
+  if (mode == 1) return v + a;
+  if (mode == 2) return a + v;
+  return v;
+}
+
 // RoPE of one dim pair (d, d + 64) at position p as transformers computes it for fp16 models: angle =
 // fp32(p * inv_freq[d]), cos and sin in fp32 rounded to fp16, x * cos + rotate_half(x) * sin with each product and
 // the sum rounded to fp16 (no contraction)

@@ -216,6 +216,14 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
 #pragma unroll
       for (int i = 0; i < R; ++i) ring[d][i] = buffer_load16_nt(wr[i], woff[i] + (wave + nwaves * d) * wstep[i]);
   }
+  // one row, one tile: the bias or residual element of the output this thread stores at the end, requested with the
+  // first weights so that its round trip is not paid after the main loop (n_out: -1 for threads that store nothing)
+  f16 aux_out{};
+  if constexpr (kFused && M == 1 && R == 1) {
+    const int n_out = nwaves == 1 ? (q == 0 && cs == 0 ? 16 * t0 + r : -1)
+                                  : ((int)threadIdx.x < RS ? 16 * t0 + RS * sub + (int)threadIdx.x : -1);
+    if ((epi.mode == kEpiBias || epi.mode == kEpiResidual) && n_out >= 0 && n_out < N) aux_out = epi.aux[n_out];
+  }
 
   // 3. stage x with the decode's own dot2 sequence run on zero weights (every nibble 8), over the lo positions
   //    (k % 8 in 0,1,4,5) and the hi positions (2,3,6,7) of each 32-k block: a block of real weights minus these is
@@ -502,7 +510,8 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
             else rope_store(n, v, up, rope_load(n));
           }
         } else if (q == 0 && cs == 0 && n < N) {
-          y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
+          if constexpr (kFused && M == 1 && R == 1) y[n] = epi_apply(epi.mode, aux_out, v);
+          else y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
         }
       }
     return;
@@ -540,7 +549,11 @@ __global__ __launch_bounds__(gemv_max_threads(M, R, D)) void gemv_mfma_layout(co
     }
     float v = 0.f;
     for (int wv2 = 0; wv2 < nwaves; ++wv2) v += red[wv2 * (R * M * RS) + idx];
-    if (n < N) y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
+    if constexpr (kFused && M == 1 && R == 1) {              // idx is threadIdx.x here (blockDim.x >= RS)
+      if (n < N) y[n] = epi_apply(epi.mode, aux_out, v);
+    } else if (n < N) {
+      y[(size_t)m * N + n] = kFused ? epi_value(epi.mode, epi.aux, v, m, n, N) : (f16)v;
+    }
   }
 }
 
