@@ -256,6 +256,19 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
         if (n + e < N) dst[e] = epi_value(epi.mode, epi.aux, v[e], m, n + e, N);
     }
   };
+  // store4 with the bias / residual elements already loaded (aux_load4)
+  auto store4_pre = [&](int m, int n, const f32x4& v, const Aux4& a) {
+    f16* dst = y + (size_t)m * N + n;
+    if (vec) {
+      const f16x2 lo = {epi_apply(epi.mode, a.v[0], v[0]), epi_apply(epi.mode, a.v[1], v[1])};
+      const f16x2 hi = {epi_apply(epi.mode, a.v[2], v[2]), epi_apply(epi.mode, a.v[3], v[3])};
+      *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = epi_apply(epi.mode, a.v[e], v[e]);
+    }
+  };
   // silu(gate rows n .. n + 3) * (up rows n + 8 .. n + 11) -> output columns 8 (n / 16) + n % 16 .. + 3
   auto store4_silu = [&](int m, int n, const f32x4& g, const f32x4& u) {
     f16* dst = y + (size_t)m * (N / 2) + 8 * (n >> 4) + (n & 15);
@@ -340,8 +353,9 @@ __global__ __launch_bounds__(64 * TW * KS) void gemm_mfma(const f16* __restrict_
       if ((n & 15) < 8) store_rope4(rope_qkv_out4(epi, m, n, split_sum(m, n), split_sum(m, n + 8)));
     } else if (epi.mode == kEpiSiluMul) {
       if ((n & 15) < 8) store4_silu(m, n, split_sum(m, n), split_sum(m, n + 8));
-    } else {
-      store4(m, n, split_sum(m, n));
+    } else {                                                // bias / residual requested with the partials
+      const Aux4 a = aux_load4(epi, m, n, N, vec);
+      store4_pre(m, n, split_sum(m, n), a);
     }
   }
 }
@@ -442,6 +456,17 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
   const int nj = (KC - wave + W - 1) / W;
 #pragma unroll
   for (int d = 0; d < D; ++d) issue(d, d);
+  // wave 0 stores the outputs: up to 32 rows, their bias / residual elements are requested with the first weights
+  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
+  constexpr bool kAuxAhead = !ROPE && MT <= 2;
+  Aux4 aux_pre[kAuxAhead ? MT : 1];
+  if constexpr (kAuxAhead) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r, n = n0 + 4 * q;
+      aux_pre[mt] = wave == 0 && m < M && n < N ? aux_load4(epi, m, n, N, vec) : Aux4{};
+    }
+  }
   if (norm) {                                               // the rows' statistics while the ring is in flight
     stage_norm_weights(epi.norm_w, 0, KC, lds_g);
     rms_rows(xr, M, K, 16 * MT, epi.norm_eps, wave, W, lane, s_rn);
@@ -488,7 +513,6 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
     for (int mt = 0; mt < MT; ++mt) store_rope4(out[mt]);
     return;
   }
-  const bool vec = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 7) == 0;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + r, n = n0 + 4 * q;
@@ -504,7 +528,18 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_tiles(const f16* __restric
     }
     if (m >= M || n >= N) continue;
     f16* dst = y + (size_t)m * N + n;
-    if (vec) {
+    if constexpr (kAuxAhead) {
+      const Aux4& a = aux_pre[mt];
+      if (vec) {
+        const f16x2 lo = {epi_apply(epi.mode, a.v[0], v[0]), epi_apply(epi.mode, a.v[1], v[1])};
+        const f16x2 hi = {epi_apply(epi.mode, a.v[2], v[2]), epi_apply(epi.mode, a.v[3], v[3])};
+        *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < N) dst[e] = epi_apply(epi.mode, a.v[e], v[e]);
+      }
+    } else if (vec) {
       const f16x2 lo = {epi_value(epi.mode, epi.aux, v[0], m, n, N), epi_value(epi.mode, epi.aux, v[1], m, n + 1, N)};
       const f16x2 hi = {epi_value(epi.mode, epi.aux, v[2], m, n + 2, N), epi_value(epi.mode, epi.aux, v[3], m, n + 3, N)};
       *reinterpret_cast<uint2*>(dst) = make_uint2(as_u32(lo), as_u32(hi));

@@ -109,6 +109,31 @@ __device__ __forceinline__ u32x4 rms_apply8(const u32x4& v, const u32x4& g, floa
   return o;
 }
 
+// The bias or residual elements of outputs n .. n + 3 of row m (what epi_value reads), loaded ahead of the sums they
+// are added to, so that their round trip overlaps the work before the store; zeros for the other modes and past N.
+// One 8-byte load where n % 4 == 0 lines up (vec: N % 4 == 0) and aux is 8-byte aligned.
+struct Aux4 {
+  f16 v[4];
+};
+__device__ __forceinline__ Aux4 aux_load4(const Epilogue& e, int m, int n, int N, bool vec) {
+  Aux4 a{};
+  if (e.mode != kEpiBias && e.mode != kEpiResidual) return a;
+  const f16* p = e.mode == kEpiBias ? e.aux + n : e.aux + (size_t)m * N + n;
+  if (vec && (reinterpret_cast<uintptr_t>(e.aux) & 7) == 0) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    const f16x2 lo = as_f16x2(u.x), hi = as_f16x2(u.y);
+    a.v[0] = lo[0];
+    a.v[1] = lo[1];
+    a.v[2] = hi[0];
+    a.v[3] = hi[1];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (n + j < N) a.v[j] = p[j];
+  }
+  return a;
+}
+
 // Four outputs of the kEpiRopeQKV epilogue, packed fp16, and where they go (dst == nullptr: nothing to store): dims
 // d .. d + 3 of a head in `lo`, their partners d + 64 .. d + 67 in `hi`, stored 64 values on.
 struct Out4 {
