@@ -667,6 +667,10 @@ def traced_gemv(a):
         return None
     rows = sorted(rows)[-n:]
     dur = [(e - b) / 1000 for b, e, _ in rows]
+    # a dispatch whose start stamp precedes the previous one's end had been queued behind it (the graph's launches are
+    # ordered): how often, and the durations counted from the later of the two stamps
+    overlaps = sum(1 for p, c in zip(rows, rows[1:]) if c[0] < p[1])
+    busy = [dur[0]] + [(c[1] - max(c[0], p[1])) / 1000 for p, c in zip(rows, rows[1:])]
     last = rows[-a.steps * len(step_projections()):]        # the final replay alone
     per = {}
     for (b, e, name), d in zip(rows, dur):
@@ -674,6 +678,7 @@ def traced_gemv(a):
         per.setdefault(key, []).append(d)
     return {"avg_us": sum(dur) / len(dur), "dispatches": len(dur),
             "traced_wall_us_per_launch": (last[-1][1] - last[0][0]) / 1000 / len(last),
+            "overlapping_dispatches": overlaps, "busy_avg_us": sum(busy) / len(busy),
             "instances": {k: {"calls": len(v), "avg_us": round(sum(v) / len(v), 3)} for k, v in sorted(per.items())}}
 
 
@@ -698,7 +703,9 @@ def roofline(trace, bytes_per_launch, graph_us, launches):
          "frac_graph": round(bytes_per_launch / (graph_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
     if trace:
         r["trace"] = {"dispatches": trace["dispatches"], "instances": trace["instances"],
-                      "traced_wall_us_per_launch": round(trace["traced_wall_us_per_launch"], 3)}
+                      "traced_wall_us_per_launch": round(trace["traced_wall_us_per_launch"], 3),
+                      "overlapping_dispatches": trace["overlapping_dispatches"],
+                      "busy_avg_us": round(trace["busy_avg_us"], 3)}
     return r
 
 
